@@ -1,0 +1,288 @@
+"""arcllm_amd -- MI355X-native (gfx950) backend for ArcLLM's packed Q4_K/Q6_K
+decode hot path.
+
+The product is the C-ABI shared library ``libarcllm_hip.so`` (declared in
+``include/arcllm_hip.h``; hand-written HIP kernels in ``csrc/``).  This module
+is the Python host mirror over that ABI, via ctypes: device buffers, streams,
+events, the kernel entry points, and the greedy ``generate`` runtime.  It
+never falls back to a CPU path: every call goes to the library, and loading
+fails loudly when the library is missing.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional
+
+import numpy as np
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libarcllm_hip.so")
+
+Q4_K = 12
+Q6_K = 14
+QK = 256
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210}
+
+ARC_OK = 0
+_STATUS = {
+    1: "INVALID_ARGUMENT",
+    2: "UNSUPPORTED",
+    3: "DEVICE",
+    4: "OUT_OF_MEMORY",
+    5: "NO_DEVICE",
+}
+
+
+class ArcError(RuntimeError):
+    """Raised when a C-ABI call returns a non-zero arc_status."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"arc_status {code} ({_STATUS.get(code, '?')}): {msg}")
+        self.code = code
+
+
+_lib: Optional[C.CDLL] = None
+
+_P = C.c_void_p
+_U32 = C.c_uint32
+_U64 = C.c_uint64
+_F = C.c_float
+_FP = C.POINTER(C.c_float)
+
+# name -> argtypes (restype int unless listed in _RESTYPE)
+_SIGS = {
+    "arc_last_error": [],
+    "arc_version": [],
+    "arc_device_count": [C.POINTER(C.c_int)],
+    "arc_set_device": [C.c_int],
+    "arc_device_info": [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t],
+    "arc_malloc": [C.POINTER(_P), C.c_size_t],
+    "arc_free": [_P],
+    "arc_memcpy_htod": [_P, _P, C.c_size_t, _P],
+    "arc_memcpy_dtoh": [_P, _P, C.c_size_t, _P],
+    "arc_memcpy_dtod": [_P, _P, C.c_size_t, _P],
+    "arc_memset": [_P, C.c_int, C.c_size_t, _P],
+    "arc_synchronize": [],
+    "arc_stream_create": [C.POINTER(_P)],
+    "arc_stream_destroy": [_P],
+    "arc_stream_synchronize": [_P],
+    "arc_event_create": [C.POINTER(_P)],
+    "arc_event_destroy": [_P],
+    "arc_event_record": [_P, _P],
+    "arc_event_elapsed_ms": [_P, _P, _FP],
+    "arc_dequant": [C.c_int, _P, _U32, _U32, _P, _P],
+    "arc_gemv": [C.c_int, _P, _U32, _U32, _P, _P, _P, _P],
+    "arc_gateup_swiglu": [C.c_int, _P, _P, _U32, _U32, _P, _P, _P],
+    "arc_gemv_splitk": [C.c_int, _P, _U32, _U32, _U32, _P, _P, _P, _P, _P],
+    "arc_rmsnorm": [_P, _P, _U32, _F, _P, _P],
+    "arc_lmhead_workspace_bytes": [C.c_int, _U32, _U32],
+    "arc_lmhead_argmax": [C.c_int, _P, _U32, _U32, _P, _P, _F, _P, _P, _P, _P],
+    "arc_synth_packed": [C.c_int, _U64, _U64, _U32, _U32, _F, _F, _P],
+    "arc_synth_normal": [_U64, _U64, C.c_size_t, _F, _F, _P],
+    "arc_tune_force": [C.c_int, C.c_int],
+}
+_RESTYPE = {
+    "arc_last_error": C.c_char_p,
+    "arc_version": C.c_char_p,
+    "arc_lmhead_workspace_bytes": C.c_size_t,
+}
+# Entry points declared in include/*.h that the tests check for.
+EXPORTED = sorted(_SIGS)
+
+
+def lib() -> C.CDLL:
+    """Load the HIP library (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ArcError(2, f"{LIB_PATH} not built (run __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        for name, args in _SIGS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPE.get(name, C.c_int)
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != ARC_OK:
+        raise ArcError(rc, lib().arc_last_error().decode(errors="replace"))
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    check(lib().arc_device_count(C.byref(n)))
+    return n.value
+
+
+def device_info() -> tuple[str, str]:
+    name = C.create_string_buffer(256)
+    arch = C.create_string_buffer(256)
+    check(lib().arc_device_info(name, 256, arch, 256))
+    return name.value.decode(), arch.value.decode()
+
+
+def synchronize() -> None:
+    check(lib().arc_synchronize())
+
+
+class DeviceBuffer:
+    """Device memory from arc_malloc, freed on close()/garbage collection."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = _P()
+        check(lib().arc_malloc(C.byref(p), max(self.nbytes, 1)))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray, stream: Optional["Stream"] = None) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a, stream)
+        return b
+
+    def upload(self, a: np.ndarray, stream: Optional["Stream"] = None) -> None:
+        a = np.ascontiguousarray(a)
+        if a.nbytes > self.nbytes:
+            raise ValueError("array larger than device buffer")
+        check(lib().arc_memcpy_htod(self.ptr, a.ctypes.data, a.nbytes, _sp(stream)))
+        if stream is None:
+            synchronize()
+
+    def download(self, dtype, count: Optional[int] = None, stream: Optional["Stream"] = None) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        n = self.nbytes // dtype.itemsize if count is None else int(count)
+        out = np.empty(n, dtype=dtype)
+        check(lib().arc_memcpy_dtoh(out.ctypes.data, self.ptr, out.nbytes, _sp(stream)))
+        return out
+
+    def zero(self, stream: Optional["Stream"] = None) -> None:
+        check(lib().arc_memset(self.ptr, 0, self.nbytes, _sp(stream)))
+
+    def close(self) -> None:
+        if getattr(self, "ptr", None):
+            if _lib is not None:
+                _lib.arc_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Stream:
+    def __init__(self):
+        p = _P()
+        check(lib().arc_stream_create(C.byref(p)))
+        self.handle = p.value
+
+    def synchronize(self) -> None:
+        check(lib().arc_stream_synchronize(self.handle))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            if _lib is not None:
+                _lib.arc_stream_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        p = _P()
+        check(lib().arc_event_create(C.byref(p)))
+        self.handle = p.value
+
+    def record(self, stream: Optional[Stream] = None) -> None:
+        check(lib().arc_event_record(self.handle, _sp(stream)))
+
+    def elapsed_ms(self, later: "Event") -> float:
+        ms = C.c_float(0.0)
+        check(lib().arc_event_elapsed_ms(self.handle, later.handle, C.byref(ms)))
+        return ms.value
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            if _lib is not None:
+                _lib.arc_event_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _sp(stream: Optional[Stream]):
+    return None if stream is None else stream.handle
+
+
+def _ptr(x) -> Optional[int]:
+    if x is None:
+        return None
+    if isinstance(x, DeviceBuffer):
+        return x.ptr
+    return int(x)
+
+
+# ------------------------------------------------------------ kernel calls
+def dequant(qtype: int, w, rows: int, K: int, out, stream: Optional[Stream] = None) -> None:
+    check(lib().arc_dequant(qtype, _ptr(w), rows, K, _ptr(out), _sp(stream)))
+
+
+def gemv(qtype: int, w, rows: int, K: int, x, y, bias=None, stream: Optional[Stream] = None) -> None:
+    check(lib().arc_gemv(qtype, _ptr(w), rows, K, _ptr(x), _ptr(bias), _ptr(y), _sp(stream)))
+
+
+def gateup_swiglu(qtype: int, w_gate, w_up, rows: int, K: int, x, s, stream: Optional[Stream] = None) -> None:
+    check(lib().arc_gateup_swiglu(qtype, _ptr(w_gate), _ptr(w_up), rows, K, _ptr(x), _ptr(s), _sp(stream)))
+
+
+def gemv_splitk(qtype: int, w, rows: int, K: int, splits: int, x, partials, y, residual=None,
+                stream: Optional[Stream] = None) -> None:
+    check(lib().arc_gemv_splitk(qtype, _ptr(w), rows, K, splits, _ptr(x), _ptr(partials), _ptr(residual),
+                                _ptr(y), _sp(stream)))
+
+
+def rmsnorm(x, w, n: int, eps: float, y, stream: Optional[Stream] = None) -> None:
+    check(lib().arc_rmsnorm(_ptr(x), _ptr(w), n, eps, _ptr(y), _sp(stream)))
+
+
+def lmhead_workspace_bytes(qtype: int, rows: int, K: int) -> int:
+    return int(lib().arc_lmhead_workspace_bytes(qtype, rows, K))
+
+
+def lmhead_argmax(qtype: int, w, rows: int, K: int, h, normw, eps: float, logits, workspace, out,
+                  stream: Optional[Stream] = None) -> None:
+    check(lib().arc_lmhead_argmax(qtype, _ptr(w), rows, K, _ptr(h), _ptr(normw), eps, _ptr(logits),
+                                  _ptr(workspace), _ptr(out), _sp(stream)))
+
+
+def tune_force(bs: int, rpl: int) -> None:
+    """Force the GEMV lane layout (bs quads per row, rpl rows per lane); 0 = automatic."""
+    check(lib().arc_tune_force(bs, rpl))
+
+
+# ------------------------------------------------------- synthetic inputs
+def synth_packed(qtype: int, seed: int, stream: int, rows: int, K: int, d_sigma: float = 0.01,
+                 dmin_sigma: float = 0.005) -> np.ndarray:
+    out = np.empty(rows * (K // QK) * BLOCK_BYTES[qtype], dtype=np.uint8)
+    check(lib().arc_synth_packed(qtype, seed, stream, rows, K, d_sigma, dmin_sigma, out.ctypes.data))
+    return out
+
+
+def synth_normal(seed: int, stream: int, n: int, mean: float = 0.0, sigma: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    check(lib().arc_synth_normal(seed, stream, n, mean, sigma, out.ctypes.data))
+    return out

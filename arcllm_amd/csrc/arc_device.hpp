@@ -1,0 +1,103 @@
+// arc_device.hpp -- gfx950 device helpers for the packed Q4_K/Q6_K kernels:
+// super-block loads, x staging layout in LDS, in-register unpacking and
+// wave64 cross-lane reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace arc {
+
+constexpr int kWave = 64;
+constexpr int kQK = 256;         // weights per super-block
+constexpr int kQ4Bytes = 144;    // Q4_K super-block
+constexpr int kQ6Bytes = 210;    // Q6_K super-block
+constexpr int kFmtQ4 = 12;
+constexpr int kFmtQ6 = 14;
+
+// --------------------------------------------------------------- x staging
+// Each super-block column of x is held in LDS as 4 lane slots of 68 floats:
+// the 64 x values one lane of a 4-lane "quad" multiplies against (four
+// groups of 16 consecutive elements), followed by the 4 group sums.  A quad
+// of lanes covers one super-block; slot v belongs to lane v of the quad.
+constexpr int kSlot = 68;
+constexpr int kXBlk = 4 * kSlot;  // 272 floats per super-block column
+
+// Element offset (within the super-block) of group t (0..3) of lane slot v.
+//  Q4_K: lane v owns 16-byte nibble chunks v and v+4; chunk c holds
+//        elements (c>>1)*64 + (c&1)*16 + i (low nibbles) and +32 (high).
+//  Q6_K: lane v owns ql chunk v of both 128-element halves; it yields
+//        quarter qa = v>>1 (low nibbles) and qa+2 (high nibbles), at
+//        l = (v&1)*16 + i.
+template <int FMT>
+__device__ __host__ constexpr int x_group_offset(int v, int t)
+{
+    if (FMT == kFmtQ4) {
+        const int c = v + 4 * (t >> 1);
+        return (c >> 1) * 64 + (t & 1) * 32 + (c & 1) * 16;
+    } else {
+        const int qa = v >> 1;
+        const int q = (t & 1) ? qa + 2 : qa;
+        return (t >> 1) * 128 + q * 32 + (v & 1) * 16;
+    }
+}
+
+// ----------------------------------------------------------------- loads
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+__device__ __forceinline__ uint4 ld16_aligned(const uint8_t* p)
+{
+    return *reinterpret_cast<const uint4*>(p);
+}
+
+// 16 bytes at a 2-byte aligned address, realigned in registers.  Reads one
+// dwordx4 and one dword from the enclosing dword-aligned span; every dword
+// read contains at least one byte of [p, p+16) or the two bytes that follow
+// p+15 within the same super-block (see the Q6_K loader for the argument).
+__device__ __forceinline__ void ld16_realign(const uint8_t* p, uint32_t out[4], uint32_t& tail)
+{
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+    const uint32_t sh = uint32_t(a & 3u);
+    const u32x4a4 v = *reinterpret_cast<const u32x4a4*>(q);
+    tail = q[4];
+    out[0] = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+    out[1] = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+    out[2] = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
+    out[3] = __builtin_amdgcn_alignbyte(tail, v.w, sh);
+    tail = tail >> (8u * sh);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits)
+{
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits & 0xffffu)));
+}
+
+__device__ __forceinline__ float byte_f(uint32_t w, int i)
+{
+    return static_cast<float>((w >> (8 * i)) & 0xffu);
+}
+
+// ------------------------------------------------------------ reductions
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+
+// Sum over aligned groups of N consecutive lanes (N a power of two <= 64);
+// every lane of the group receives the group total.  The combination order
+// is fixed, so results are deterministic.
+template <int N>
+__device__ __forceinline__ float group_sum(float v)
+{
+    if constexpr (N >= 2) v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]: lane ^ 1
+    if constexpr (N >= 4) v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]: lane ^ 2
+    if constexpr (N >= 8) v += dpp_f<0x141>(v);   // row_half_mirror: other quad of 8
+    if constexpr (N >= 16) v += dpp_f<0x140>(v);  // row_mirror: other 8 of 16
+    if constexpr (N >= 32) v += __shfl_xor(v, 16);
+    if constexpr (N >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+}  // namespace arc

@@ -1,0 +1,158 @@
+/*
+ * arcllm_hip.h -- C ABI of the MI355X (gfx950) backend for ArcLLM's packed
+ * Q4_K/Q6_K decode hot path.
+ *
+ * Plain C: pointers, sizes and int status codes.  No exception and no C++
+ * or torch type crosses this boundary.  Every call returns ARC_OK (0) or an
+ * arc_status code; arc_last_error() then holds a thread-local message.
+ *
+ * Device pointers come from arc_malloc (or any hipMalloc'd memory of the same
+ * process).  Kernel entry points are asynchronous on the given stream (NULL =
+ * the default stream); results are visible after arc_stream_synchronize /
+ * arc_synchronize.  A stream (and everything launched on it) is used by one
+ * host thread at a time.
+ *
+ * Packed tensors are GGUF row-major: a weight of rows x K (K a multiple of
+ * 256) is rows * (K/256) super-blocks, 144 bytes each for Q4_K
+ *   (d f16 @0, dmin f16 @2, 12 bytes 6-bit scales/mins @4, 128 bytes nibbles @16)
+ * and 210 bytes each for Q6_K
+ *   (ql[128] @0, qh[64] @128, int8 scales[16] @192, d f16 @208).
+ * Q4_K tensors must start 16-byte aligned, Q6_K tensors 2-byte aligned (GGUF
+ * data is 32-byte aligned).  fp32 vectors must be 16-byte aligned.
+ *
+ * Reference interfaces replaced (minhtri22/ArcLLM):
+ *   device runtime   VkRuntime::{init,make_buffer,execute_prepared}
+ *                    src/arcllm_v1_vulkan_runtime_support.h:498-704
+ *   kernel contract  PCGemm{n,rows,batch,row_bytes,add_bias,w_base_bytes,bias_base}
+ *                    src/arcllm_v1_runtime.cpp:268-277, dispatches :371-421
+ */
+#ifndef ARCLLM_HIP_H
+#define ARCLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum arc_status {
+    ARC_OK = 0,
+    ARC_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size or alignment */
+    ARC_ERR_UNSUPPORTED = 2,      /* shape or type outside what the kernels implement */
+    ARC_ERR_DEVICE = 3,           /* HIP runtime error (message in arc_last_error) */
+    ARC_ERR_OUT_OF_MEMORY = 4,
+    ARC_ERR_NO_DEVICE = 5
+} arc_status;
+
+typedef enum arc_qtype {
+    ARC_Q4_K = 12, /* ggml type id of Q4_K (src/arcllm_v1_runtime.cpp:168) */
+    ARC_Q6_K = 14  /* ggml type id of Q6_K */
+} arc_qtype;
+
+typedef void *arc_stream_t; /* a hipStream_t; NULL is the default stream */
+typedef void *arc_event_t;  /* a hipEvent_t */
+
+/* ---------------------------------------------------------------- runtime */
+const char *arc_last_error(void);
+const char *arc_version(void);
+/* Number of HIP devices visible (0 without a GPU; never an error then). */
+int arc_device_count(int *count);
+int arc_set_device(int device);
+/* Device name and gfx architecture string of the current device. */
+int arc_device_info(char *name, size_t name_len, char *arch, size_t arch_len);
+
+int arc_malloc(void **ptr, size_t bytes);
+int arc_free(void *ptr);
+int arc_memcpy_htod(void *dst, const void *src, size_t bytes, arc_stream_t stream);
+int arc_memcpy_dtoh(void *dst, const void *src, size_t bytes, arc_stream_t stream);
+int arc_memcpy_dtod(void *dst, const void *src, size_t bytes, arc_stream_t stream);
+int arc_memset(void *dst, int value, size_t bytes, arc_stream_t stream);
+int arc_synchronize(void);
+
+int arc_stream_create(arc_stream_t *stream);
+int arc_stream_destroy(arc_stream_t stream);
+int arc_stream_synchronize(arc_stream_t stream);
+int arc_event_create(arc_event_t *event);
+int arc_event_destroy(arc_event_t event);
+int arc_event_record(arc_event_t event, arc_stream_t stream);
+int arc_event_elapsed_ms(arc_event_t start, arc_event_t stop, float *ms);
+
+/* ------------------------------------------------------- element decode */
+/* out[r*K + k] = fp32 weight, bit-exact with the reference CPU decode:
+ * Q4_K  w = d*sc*q - dmin*mn   (src/sa1_component_benchmark.cpp:105-116)
+ * Q6_K  w = d*scale*q          (src/q6cb_q6_reference.hpp:49-91)
+ * each product/difference rounded separately, left to right. */
+int arc_dequant(int qtype, const void *w, uint32_t rows, uint32_t K, float *out,
+                arc_stream_t stream);
+
+/* ------------------------------------------------------------------ GEMV */
+/* y[r] = sum_k w[r,k] * x[k] (+ bias[r] when bias != NULL), fp32 accumulate.
+ * Replaces the decode q/k/v/o, gate/up and Q6 down dispatches of
+ * shaders/p7_q4k_gemm_2d.comp, shaders/sa1_q4k_subgroup_splitk.comp and
+ * shaders/p7_q6k_gemm_2d.comp (src/arcllm_v1_runtime.cpp:380-413). */
+int arc_gemv(int qtype, const void *w, uint32_t rows, uint32_t K, const float *x,
+             const float *bias, float *y, arc_stream_t stream);
+
+/* Fused FFN gate/up + SwiGLU on Q4_K: s[r] = silu(gate[r].x) * (up[r].x),
+ * silu(g) = g / (1 + exp(-g)).  Replaces the ffn_gate + ffn_up + swiglu
+ * dispatches (src/arcllm_v1_runtime.cpp:390-409, shaders/p7_swiglu.comp). */
+int arc_gateup_swiglu(int qtype, const void *w_gate, const void *w_up, uint32_t rows,
+                      uint32_t K, const float *x, float *s, arc_stream_t stream);
+
+/* Split-K GEMV with a deterministic two-pass reduction.  Pass 1 writes
+ * partials[j*rows + r] for split j over super-block columns
+ * [j*bps, min((j+1)*bps, K/256)), bps = ceil((K/256)/splits); pass 2 sums
+ * the partials of each row in order j = 0..splits-1 (no atomics), and adds
+ * residual[r] last when residual != NULL.  partials holds splits*rows floats.
+ * Replaces the ffn_down dispatch and the Q4 down backend route
+ * (src/arcllm_v1_runtime.cpp:405-413,
+ *  src/arcllm_v1_q4_vulkan_backend_v4_runtime.h:347-386). */
+int arc_gemv_splitk(int qtype, const void *w, uint32_t rows, uint32_t K, uint32_t splits,
+                    const float *x, float *partials, const float *residual, float *y,
+                    arc_stream_t stream);
+
+/* ------------------------------------------------------- norm / LM head */
+/* y = x * rsqrt(mean(x^2) + eps) * w over n elements (shaders/p7_rmsnorm_seq.comp). */
+int arc_rmsnorm(const float *x, const float *w, uint32_t n, float eps, float *y,
+                arc_stream_t stream);
+
+/* Bytes of device workspace arc_lmhead_argmax needs for `rows` vocabulary rows. */
+size_t arc_lmhead_workspace_bytes(int qtype, uint32_t rows, uint32_t K);
+
+/* Greedy LM-head step on the GPU: x = RMSNorm(h; normw, eps), logits =
+ * W.x, out[0] = argmax with ties to the LOWEST index over finite logits,
+ * out[1] = number of non-finite logits (0 when all are finite).
+ * logits may be NULL (not materialised).  workspace: device memory of
+ * arc_lmhead_workspace_bytes() bytes.  normw == NULL skips the norm.
+ * Replaces append_lm (src/arcllm_v1_runtime.cpp:285-291,
+ * shaders/p8q1_lmhead_q6k_segmented_chunk.comp) plus the host argmax
+ * runtime_top2 (src/arcllm_v1_runtime.cpp:132-148,499-504). */
+int arc_lmhead_argmax(int qtype, const void *w, uint32_t rows, uint32_t K, const float *h,
+                      const float *normw, float eps, float *logits, void *workspace,
+                      uint32_t *out, arc_stream_t stream);
+
+/* Tuning hook: force the GEMV lane layout for later launches on this host
+ * thread (bs = super-block quads per row: 1,2,4,8,16; rpl = rows per lane:
+ * 1,2,4).  bs = 0 restores the automatic choice. */
+int arc_tune_force(int bs, int rpl);
+
+/* ------------------------------------------------------ synthetic inputs */
+/* Host-side, deterministic generators for seeded synthetic packed tensors
+ * (no GPU needed).  Each super-block draws from splitmix64 seeded by
+ * (seed, stream, block index), so any slice can be regenerated alone.
+ * Q4_K: d = f16(|N(0, d_sigma)|), dmin = f16(|N(0, dmin_sigma)|), the 140
+ *       scale/min and nibble bytes uniform.
+ * Q6_K: ql/qh uniform bits, int8 scales uniform in [-32, 31],
+ *       d = f16(|N(0, d_sigma)|).
+ * `out` is host memory of rows*(K/256)*block_bytes bytes. */
+int arc_synth_packed(int qtype, uint64_t seed, uint64_t stream, uint32_t rows, uint32_t K,
+                     float d_sigma, float dmin_sigma, void *out);
+/* out[i] = float(mean + sigma * N(0,1)), element i drawn from (seed, stream, i). */
+int arc_synth_normal(uint64_t seed, uint64_t stream, size_t n, float mean, float sigma,
+                     float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ARCLLM_HIP_H */

@@ -1,0 +1,401 @@
+/*
+ * arc_oracle.c -- CPU oracle (TEST INFRASTRUCTURE ONLY; see arc_oracle.h).
+ *
+ * Plain-C restatement of the reference's CPU arithmetic for the packed
+ * Q4_K/Q6_K decode path.  Citations are to the reference tree
+ * (minhtri22/ArcLLM).  Compiled with -ffp-contract=off so every float
+ * expression rounds exactly as written, as under MSVC /fp:precise.
+ */
+#include "arc_oracle.h"
+
+#include <math.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* IEEE binary16 -> binary32.  src/q6cb_q6_reference.hpp:20-36 and
+ * src/sa1_component_benchmark.cpp:84-94: subnormals via ldexp(frac, -24),
+ * +-inf, any NaN payload -> the canonical quiet NaN. */
+float orc_half_to_float(uint16_t h)
+{
+    const uint32_t sign = (h >> 15) & 1u, ex = (h >> 10) & 31u, frac = h & 1023u;
+    float v;
+    if (ex == 0u) {
+        if (frac == 0u) return sign ? -0.0f : 0.0f;
+        v = ldexpf((float)frac, -24);
+        return sign ? -v : v;
+    }
+    if (ex == 31u) {
+        if (frac) return NAN;
+        return sign ? -INFINITY : INFINITY;
+    }
+    v = ldexpf(1.0f + (float)frac / 1024.0f, (int)ex - 15);
+    return sign ? -v : v;
+}
+
+/* binary32 -> binary16, round to nearest even (overflow -> inf, NaN kept
+ * quiet).  Used where the reference path stores a value as fp16 (the KV
+ * cache of the MI355X runtime). */
+uint16_t orc_float_to_half_rne(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) /* inf or NaN */
+        return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u | ((ax >> 13) & 0x3ffu) : 0u));
+    if (ax >= 0x477ff000u) /* rounds to >= 65520 -> inf */
+        return (uint16_t)(sign | 0x7c00u);
+    if (ax < 0x38800000u) { /* result is subnormal or zero: value = ax * 2^24 in units of 2^-24 */
+        const uint32_t e = ax >> 23;
+        if (e < 102u) return (uint16_t)sign; /* < 2^-25: rounds to 0 */
+        const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        const uint32_t shift = 126u - e; /* 14..24 */
+        uint32_t r = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (r & 1u))) ++r;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = ((ax >> 13) - (112u << 10));
+    const uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
+    return (uint16_t)(sign | r);
+}
+
+static uint16_t ld16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* Q4_K 6-bit scale/min of sub-block j (0..7) from the 12 packed bytes at
+ * block offset 4.  src/sa1_component_benchmark.cpp:97-104,
+ * src/arcllm_v1_i001r_p8c_profile_runtime.cpp:563-572. */
+void orc_q4k_scale_min(const uint8_t *blk, uint32_t j, uint32_t *sc, uint32_t *mn)
+{
+    const uint8_t *s = blk + 4;
+    if (j < 4u) {
+        *sc = s[j] & 63u;
+        *mn = s[j + 4] & 63u;
+    } else {
+        *sc = (uint32_t)(s[j + 4] & 15u) | ((uint32_t)(s[j - 4] >> 6) << 4);
+        *mn = (uint32_t)(s[j + 4] >> 4) | ((uint32_t)(s[j] >> 6) << 4);
+    }
+}
+
+/* 4-bit code of element k (0..255): byte 16 + (k>>6)*32 + (k&31), low
+ * nibble when (k&63) < 32.  src/sa1_component_benchmark.cpp:113-114. */
+uint32_t orc_q4k_code(const uint8_t *blk, uint32_t k)
+{
+    const uint32_t local64 = k & 63u;
+    const uint8_t qb = blk[16u + (k >> 6) * 32u + (local64 & 31u)];
+    return local64 < 32u ? (qb & 15u) : (qb >> 4u);
+}
+
+/* w = d*sc*q - dmin*mn, evaluated left to right in fp32 without
+ * contraction.  src/sa1_component_benchmark.cpp:105-116,
+ * shaders/sa1_q4k_subgroup_splitk.comp:48-61. */
+float orc_q4k_weight(const uint8_t *blk, uint32_t k)
+{
+    const float d = orc_half_to_float(ld16(blk));
+    const float dmin = orc_half_to_float(ld16(blk + 2));
+    uint32_t sc, mn;
+    orc_q4k_scale_min(blk, k >> 5, &sc, &mn);
+    const uint32_t q = orc_q4k_code(blk, k);
+    const float a = d * (float)sc;
+    const float b = a * (float)q;
+    const float c = dmin * (float)mn;
+    return b - c;
+}
+
+/* Q6_K code and scale of element k.  src/q6cb_q6_reference.hpp:49-91,
+ * src/sa1_component_benchmark.cpp:118-130. */
+int orc_q6k_code(const uint8_t *blk, uint32_t k, int *scale)
+{
+    const uint32_t half = k >> 7, kk = k & 127u, l = kk & 31u, quarter = kk >> 5;
+    const uint8_t *ql = blk + half * 64u;
+    const uint8_t *qh = blk + 128u + half * 32u;
+    const uint8_t *sc = blk + 192u + half * 8u;
+    const uint32_t is = l >> 4;
+    uint32_t low, high, si;
+    switch (quarter) {
+    case 0: low = ql[l] & 15u; high = qh[l] & 3u; si = is; break;
+    case 1: low = ql[l + 32u] & 15u; high = (qh[l] >> 2) & 3u; si = is + 2u; break;
+    case 2: low = ql[l] >> 4; high = (qh[l] >> 4) & 3u; si = is + 4u; break;
+    default: low = ql[l + 32u] >> 4; high = (qh[l] >> 6) & 3u; si = is + 6u; break;
+    }
+    *scale = (int)(int8_t)sc[si];
+    return (int)(low | (high << 4)) - 32;
+}
+
+/* w = d*scale*q in fp32, left to right.  src/q6cb_q6_reference.hpp:86-89. */
+float orc_q6k_weight(const uint8_t *blk, uint32_t k)
+{
+    int scale;
+    const int q = orc_q6k_code(blk, k, &scale);
+    const float d = orc_half_to_float(ld16(blk + 208));
+    const float a = d * (float)scale;
+    return a * (float)q;
+}
+
+static int row_bytes(int qtype, uint32_t K, size_t *rb, size_t *bb)
+{
+    if (K == 0u || (K % ORC_QK) != 0u) return -1;
+    if (qtype == ORC_Q4_K) *bb = ORC_Q4K_BLOCK_BYTES;
+    else if (qtype == ORC_Q6_K) *bb = ORC_Q6K_BLOCK_BYTES;
+    else return -1;
+    *rb = (size_t)(K / ORC_QK) * *bb;
+    return 0;
+}
+
+static float weight_at(int qtype, const uint8_t *blk, uint32_t k)
+{
+    return qtype == ORC_Q4_K ? orc_q4k_weight(blk, k) : orc_q6k_weight(blk, k);
+}
+
+int orc_dequant(int qtype, const uint8_t *w, uint32_t rows, uint32_t K, float *out)
+{
+    size_t rb, bb;
+    if (row_bytes(qtype, K, &rb, &bb)) return -1;
+    for (uint32_t r = 0; r < rows; ++r)
+        for (uint32_t k = 0; k < K; ++k)
+            out[(size_t)r * K + k] = weight_at(qtype, w + r * rb + (k / ORC_QK) * bb, k % ORC_QK);
+    return 0;
+}
+
+/* Serial fp32 dot, sum initialised with the bias: shaders/p7_q4k_gemm_2d.comp:13,
+ * shaders/p7_q6k_gemm_2d.comp, src/sa1_component_benchmark.cpp:165-173. */
+static float dot_r0(int qtype, const uint8_t *row, size_t bb, uint32_t K, const float *x, float init)
+{
+    float sum = init;
+    for (uint32_t k = 0; k < K; ++k) {
+        const float p = weight_at(qtype, row + (k / ORC_QK) * bb, k % ORC_QK) * x[k];
+        sum = sum + p;
+    }
+    return sum;
+}
+
+int orc_gemv_r0(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
+                const float *x, const float *bias, float *y)
+{
+    size_t rb, bb;
+    if (row_bytes(qtype, K, &rb, &bb)) return -1;
+    for (uint32_t r = 0; r < rows; ++r)
+        y[r] = dot_r0(qtype, w + r * rb, bb, K, x, bias ? bias[r] : 0.0f);
+    return 0;
+}
+
+int orc_gemv_r0_mt(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
+                   const float *x, const float *bias, float *y, int nthreads)
+{
+    size_t rb, bb;
+    if (row_bytes(qtype, K, &rb, &bb)) return -1;
+    long r;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1)
+#endif
+    for (r = 0; r < (long)rows; ++r)
+        y[r] = dot_r0(qtype, w + (size_t)r * rb, bb, K, x, bias ? bias[r] : 0.0f);
+    (void)nthreads;
+    return 0;
+}
+
+/* fp64 accumulation over fp32-decoded weights: src/q6cb_q6_reference.hpp:118-132. */
+int orc_gemv_r64(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
+                 const float *x, const float *bias, double *y)
+{
+    size_t rb, bb;
+    if (row_bytes(qtype, K, &rb, &bb)) return -1;
+    long r;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (r = 0; r < (long)rows; ++r) {
+        const uint8_t *row = w + (size_t)r * rb;
+        double sum = 0.0;
+        for (uint32_t k = 0; k < K; ++k)
+            sum += (double)weight_at(qtype, row + (k / ORC_QK) * bb, k % ORC_QK) * (double)x[k];
+        y[r] = sum + (bias ? (double)bias[r] : 0.0);
+    }
+    return 0;
+}
+
+int orc_gemv_r64_xd(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
+                    const double *x, double *y)
+{
+    size_t rb, bb;
+    if (row_bytes(qtype, K, &rb, &bb)) return -1;
+    long r;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (r = 0; r < (long)rows; ++r) {
+        const uint8_t *row = w + (size_t)r * rb;
+        double sum = 0.0;
+        for (uint32_t k = 0; k < K; ++k)
+            sum += (double)weight_at(qtype, row + (k / ORC_QK) * bb, k % ORC_QK) * x[k];
+        y[r] = sum;
+    }
+    return 0;
+}
+
+int orc_gemv_splitk_r64(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
+                        uint32_t splits, const float *x, double *part)
+{
+    size_t rb, bb;
+    if (row_bytes(qtype, K, &rb, &bb) || splits == 0u) return -1;
+    const uint32_t nb = K / ORC_QK;
+    const uint32_t bps = (nb + splits - 1u) / splits;
+    long r;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (r = 0; r < (long)rows; ++r) {
+        const uint8_t *row = w + (size_t)r * rb;
+        for (uint32_t s = 0; s < splits; ++s) {
+            double sum = 0.0;
+            const uint32_t b0 = s * bps, b1 = (s + 1u) * bps < nb ? (s + 1u) * bps : nb;
+            for (uint32_t b = b0; b < b1; ++b)
+                for (uint32_t k = 0; k < ORC_QK; ++k)
+                    sum += (double)weight_at(qtype, row + b * bb, k) * (double)x[b * ORC_QK + k];
+            part[(size_t)s * rows + (size_t)r] = sum;
+        }
+    }
+    return 0;
+}
+
+/* RMSNorm: fp64 sum of squares, float rsqrt, y = x*inv*w.
+ * src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1115-1126. */
+void orc_rmsnorm_f32(const float *x, const float *w, uint32_t n, float eps, float *y)
+{
+    double ss = 0.0;
+    for (uint32_t i = 0; i < n; ++i) ss += (double)x[i] * (double)x[i];
+    const float mean = (float)(ss / (double)n);
+    const float inv = 1.0f / sqrtf(mean + eps);
+    for (uint32_t i = 0; i < n; ++i) {
+        const float t = x[i] * inv;
+        y[i] = t * w[i];
+    }
+}
+
+void orc_rmsnorm_f64(const double *x, const float *w, uint32_t n, double eps, double *y)
+{
+    double ss = 0.0;
+    for (uint32_t i = 0; i < n; ++i) ss += x[i] * x[i];
+    const double inv = 1.0 / sqrt(ss / (double)n + eps);
+    for (uint32_t i = 0; i < n; ++i) y[i] = x[i] * inv * (double)w[i];
+}
+
+/* s = (g / (1 + exp(-g))) * u.  src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1221-1230,
+ * shaders/p7_swiglu.comp:7-12. */
+void orc_swiglu_f32(const float *g, const float *u, uint32_t n, float *s)
+{
+    for (uint32_t i = 0; i < n; ++i) {
+        const float d = 1.0f + expf(-g[i]);
+        const float a = g[i] / d;
+        s[i] = a * u[i];
+    }
+}
+
+void orc_swiglu_f64(const double *g, const double *u, uint32_t n, double *s)
+{
+    for (uint32_t i = 0; i < n; ++i) s[i] = (g[i] / (1.0 + exp(-g[i]))) * u[i];
+}
+
+/* RoPE on ADJACENT pairs (2p, 2p+1) of each head, angle = pos * theta^(-2p/dim).
+ * src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1158-1175, shaders/p7_rope_seq.comp:27-37. */
+void orc_rope_f32(float *x, uint32_t heads, uint32_t dim, uint32_t pos, float theta)
+{
+    for (uint32_t h = 0; h < heads; ++h) {
+        float *base = x + (size_t)h * dim;
+        for (uint32_t p = 0; p < dim / 2u; ++p) {
+            const float ex = -2.0f * (float)p / (float)dim;
+            const float angle = (float)pos * powf(theta, ex);
+            const float c = cosf(angle), s = sinf(angle);
+            const float a = base[2 * p], b = base[2 * p + 1];
+            const float ac = a * c, bs = b * s, as = a * s, bc = b * c;
+            base[2 * p] = ac - bs;
+            base[2 * p + 1] = as + bc;
+        }
+    }
+}
+
+void orc_rope_f64(double *x, uint32_t heads, uint32_t dim, uint32_t pos, double theta)
+{
+    for (uint32_t h = 0; h < heads; ++h) {
+        double *base = x + (size_t)h * dim;
+        for (uint32_t p = 0; p < dim / 2u; ++p) {
+            const double angle = (double)pos * pow(theta, -2.0 * (double)p / (double)dim);
+            const double c = cos(angle), s = sin(angle);
+            const double a = base[2 * p], b = base[2 * p + 1];
+            base[2 * p] = a * c - b * s;
+            base[2 * p + 1] = a * s + b * c;
+        }
+    }
+}
+
+/* Top-1/top-2 with strict '>' (ties go to the lowest index); non-finite
+ * logits are skipped and clear the finite flag.  src/arcllm_v1_runtime.cpp:132-148. */
+void orc_top2(const float *p, uint32_t n, orc_top2_t *r)
+{
+    r->top1 = r->top2 = 0;
+    r->logit1 = r->logit2 = -INFINITY;
+    r->finite = 1;
+    for (uint32_t i = 0; i < n; ++i) {
+        const float v = p[i];
+        if (!isfinite(v)) { r->finite = 0; continue; }
+        if (v > r->logit1) {
+            r->logit2 = r->logit1; r->top2 = r->top1;
+            r->logit1 = v; r->top1 = i;
+        } else if (v > r->logit2) {
+            r->logit2 = v; r->top2 = i;
+        }
+    }
+    if (!isfinite(r->logit1) || !isfinite(r->logit2)) r->finite = 0;
+}
+
+void orc_top2_f64(const double *p, uint32_t n, uint32_t *t1, uint32_t *t2, double *l1, double *l2)
+{
+    *t1 = *t2 = 0;
+    *l1 = *l2 = -INFINITY;
+    for (uint32_t i = 0; i < n; ++i) {
+        const double v = p[i];
+        if (!isfinite(v)) continue;
+        if (v > *l1) { *l2 = *l1; *t2 = *t1; *l1 = v; *t1 = i; }
+        else if (v > *l2) { *l2 = v; *t2 = i; }
+    }
+}
+
+/* Cached GQA for one query position: fp64 dot products and softmax over
+ * positions 0..pos, kv head = q head / (qh/kvh).
+ * src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1177-1212 (causal row t = pos),
+ * cache addressing shaders/p7_attention_kv_online.comp (layer slice
+ * [ctx][kvh][dim]).  Keys and values are the fp16 cache contents. */
+void orc_attention_decode_f64(const double *q, const uint16_t *kc, const uint16_t *vc,
+                              uint32_t pos, uint32_t qh, uint32_t kvh, uint32_t dim,
+                              double *out)
+{
+    const uint32_t hpk = qh / kvh;
+    const double scale = 1.0 / sqrt((double)dim);
+    const uint32_t T = pos + 1u;
+    for (uint32_t h = 0; h < qh; ++h) {
+        const uint32_t kh = h / hpk;
+        double mx = -INFINITY, sum = 0.0;
+        /* two passes over the keys: max, then exp-sum and weighted values */
+        for (uint32_t t = 0; t < T; ++t) {
+            const uint16_t *k = kc + ((size_t)t * kvh + kh) * dim;
+            double dot = 0.0;
+            for (uint32_t d = 0; d < dim; ++d) dot += q[h * dim + d] * (double)orc_half_to_float(k[d]);
+            const double z = dot * scale;
+            if (z > mx) mx = z;
+        }
+        for (uint32_t d = 0; d < dim; ++d) out[h * dim + d] = 0.0;
+        for (uint32_t t = 0; t < T; ++t) {
+            const uint16_t *k = kc + ((size_t)t * kvh + kh) * dim;
+            const uint16_t *v = vc + ((size_t)t * kvh + kh) * dim;
+            double dot = 0.0;
+            for (uint32_t d = 0; d < dim; ++d) dot += q[h * dim + d] * (double)orc_half_to_float(k[d]);
+            const double e = exp(dot * scale - mx);
+            sum += e;
+            for (uint32_t d = 0; d < dim; ++d) out[h * dim + d] += e * (double)orc_half_to_float(v[d]);
+        }
+        for (uint32_t d = 0; d < dim; ++d) out[h * dim + d] /= sum;
+    }
+}
