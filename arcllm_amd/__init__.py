@@ -81,6 +81,7 @@ _SIGS = {
     "arc_synth_packed": [C.c_int, _U64, _U64, _U32, _U32, _F, _F, _P],
     "arc_synth_normal": [_U64, _U64, C.c_size_t, _F, _F, _P],
     "arc_tune_force": [C.c_int, C.c_int],
+    "arc_probe_read": [_P, C.c_size_t, _P, _U32, _P],
 }
 _RESTYPE = {
     "arc_last_error": C.c_char_p,
@@ -267,6 +268,11 @@ def lmhead_argmax(qtype: int, w, rows: int, K: int, h, normw, eps: float, logits
                   stream: Optional[Stream] = None) -> None:
     check(lib().arc_lmhead_argmax(qtype, _ptr(w), rows, K, _ptr(h), _ptr(normw), eps, _ptr(logits),
                                   _ptr(workspace), _ptr(out), _sp(stream)))
+
+
+def probe_read(buf, nbytes: int, out, grid: int = 2048, stream: Optional[Stream] = None) -> None:
+    """Streaming-read probe (practical HBM read ceiling); `out` holds grid*256 uint32."""
+    check(lib().arc_probe_read(_ptr(buf), nbytes, _ptr(out), grid, _sp(stream)))
 
 
 def tune_force(bs: int, rpl: int) -> None:

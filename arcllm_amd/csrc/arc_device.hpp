@@ -44,28 +44,35 @@ __device__ __host__ constexpr int x_group_offset(int v, int t)
 
 // ----------------------------------------------------------------- loads
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint4 ld16_aligned(const uint8_t* p)
 {
     return *reinterpret_cast<const uint4*>(p);
 }
 
-// 16 bytes at a 2-byte aligned address, realigned in registers.  Reads one
-// dwordx4 and one dword from the enclosing dword-aligned span; every dword
-// read contains at least one byte of [p, p+16) or the two bytes that follow
-// p+15 within the same super-block (see the Q6_K loader for the argument).
-__device__ __forceinline__ void ld16_realign(const uint8_t* p, uint32_t out[4], uint32_t& tail)
+// 16 bytes that start `sh` bytes (0 or 2) past the dword-aligned address a4,
+// realigned in registers from one dwordx4 and the following dword.  `tail`
+// returns that following dword shifted down by sh bytes.  a4 is derived from
+// the block pointer by pointer arithmetic so the loads stay global_load.
+__device__ __forceinline__ void ld16_shifted(const uint8_t* a4, uint32_t sh, uint32_t out[4], uint32_t& tail)
 {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-    const uint32_t sh = uint32_t(a & 3u);
-    const u32x4a4 v = *reinterpret_cast<const u32x4a4*>(q);
-    tail = q[4];
+    const u32x4a4 v = *reinterpret_cast<const u32x4a4*>(a4);
+    const uint32_t t = *reinterpret_cast<const uint32_t*>(a4 + 16);
     out[0] = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
     out[1] = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
     out[2] = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
-    out[3] = __builtin_amdgcn_alignbyte(tail, v.w, sh);
-    tail = tail >> (8u * sh);
+    out[3] = __builtin_amdgcn_alignbyte(t, v.w, sh);
+    tail = t >> (8u * sh);
+}
+
+// Hides a value from instruction combining: after masking a word of 4-bit
+// codes, this keeps the mask as one v_and so each byte converts with a
+// single v_cvt_f32_ubyteN (instead of a v_bfe_u32 + v_cvt per element).
+__device__ __forceinline__ uint32_t opaque(uint32_t v)
+{
+    asm("" : "+v"(v));
+    return v;
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits)

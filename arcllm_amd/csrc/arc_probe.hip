@@ -1,0 +1,38 @@
+// arc_probe.hip -- streaming-read probe: the practical HBM read ceiling of
+// the device for a given buffer size, used by bench.py to put the GEMV
+// numbers next to what a plain coalesced read achieves on the same box.
+#include "../../include/arcllm_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+namespace arc {
+int set_error(int code, const char* fmt, ...);
+int check_hip(hipError_t e, const char* what);
+
+// Each lane reads 16-byte chunks in a grid-stride loop (one 1 KB coalesced
+// access per wave instruction) and folds them with xor; one store per lane.
+__global__ __launch_bounds__(256) void k_probe_read(const uint4* __restrict__ p, uint64_t n16,
+                                                    uint32_t* __restrict__ out)
+{
+    uint64_t i = blockIdx.x * 256ull + threadIdx.x;
+    const uint64_t stride = gridDim.x * 256ull;
+    uint32_t acc = 0;
+    for (; i < n16; i += stride) {
+        const uint4 v = p[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    out[blockIdx.x * 256u + threadIdx.x] = acc;
+}
+}  // namespace arc
+
+extern "C" int arc_probe_read(const void* p, size_t bytes, uint32_t* out, uint32_t grid, arc_stream_t stream)
+{
+    if (!p || !out || bytes < 16 || grid == 0 || grid > 65536)
+        return arc::set_error(ARC_ERR_INVALID_ARGUMENT, "bad probe arguments");
+    if (reinterpret_cast<uintptr_t>(p) & 15u) return arc::set_error(ARC_ERR_INVALID_ARGUMENT, "probe buffer not 16-byte aligned");
+    hipLaunchKernelGGL(arc::k_probe_read, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint4*>(p), uint64_t(bytes / 16), out);
+    return arc::check_hip(hipGetLastError(), "probe launch");
+}

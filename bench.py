@@ -180,6 +180,18 @@ def main() -> int:
     log(f"step {ms * 1e3:.2f} us ({gbs:.1f} GB/s); gate/up {ms_gu * 1e3:.2f} us ({ach:.1f} GB/s); "
         f"down {ms_dn * 1e3:.2f} us ({BYTES_DOWN / (ms_dn / 1e3) / 1e9:.1f} GB/s)")
 
+    # practical read ceiling of this box at the same byte counts, same rotation
+    probe_out = arc.DeviceBuffer(2048 * 256 * 4)
+    probe = [arc.DeviceBuffer(BYTES_STEP // 4096 * 4096) for _ in range(B)]
+    ms_c_step = time_loop(lambda i: arc.probe_read(probe[i % B], probe[i % B].nbytes, probe_out, 2048, stream),
+                          args.steps, stream)
+    ms_c_gu = time_loop(lambda i: arc.probe_read(probe[i % B], BYTES_GATEUP // 4096 * 4096, probe_out, 2048, stream),
+                        args.steps, stream)
+    del probe
+    ceil_step = (BYTES_STEP // 4096 * 4096) / (ms_c_step / 1e3) / 1e9
+    ceil_gu = (BYTES_GATEUP // 4096 * 4096) / (ms_c_gu / 1e3) / 1e9
+    log(f"stream-read ceiling: {ceil_step:.0f} GB/s at {BYTES_STEP} B, {ceil_gu:.0f} GB/s at {BYTES_GATEUP} B")
+
     traffic = load_traffic()
     result = {
         "metric": "Q4_K/Q6_K GEMV HBM GB/s (% of peak); 7B-shape decode tokens/s, 1 MI355X",
@@ -211,6 +223,13 @@ def main() -> int:
             "traffic": traffic.get("bytes_per_launch") if traffic else None,
             "avg_launch_us": round(ms_gu * 1e3, 3),
             "algorithmic_bytes_per_launch": BYTES_GATEUP,
+        },
+        "stream_ceiling": {
+            "kernel": "arc_probe_read (coalesced 16 B/lane streaming read, same bank rotation)",
+            "GB/s_at_step_bytes": round(ceil_step, 1),
+            "GB/s_at_gateup_bytes": round(ceil_gu, 1),
+            "value_frac_of_ceiling": round(gbs / ceil_step, 4),
+            "roofline_frac_of_ceiling": round(ach / ceil_gu, 4),
         },
         "device": f"{name} {gfx}",
     }

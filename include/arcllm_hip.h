@@ -101,10 +101,11 @@ int arc_gateup_swiglu(int qtype, const void *w_gate, const void *w_up, uint32_t 
                       uint32_t K, const float *x, float *s, arc_stream_t stream);
 
 /* Split-K GEMV with a deterministic two-pass reduction.  Pass 1 writes
- * partials[j*rows + r] for split j over super-block columns
+ * partials[r*used + j] for split j over super-block columns
  * [j*bps, min((j+1)*bps, K/256)), bps = ceil((K/256)/splits); pass 2 sums
- * the partials of each row in order j = 0..splits-1 (no atomics), and adds
- * residual[r] last when residual != NULL.  partials holds splits*rows floats.
+ * the partials of each row in order j = 0..used-1 (no atomics), and adds
+ * residual[r] last when residual != NULL.  used = ceil((K/256)/bps) (splits
+ * that would own no column are dropped).  partials holds splits*rows floats.
  * Replaces the ffn_down dispatch and the Q4 down backend route
  * (src/arcllm_v1_runtime.cpp:405-413,
  *  src/arcllm_v1_q4_vulkan_backend_v4_runtime.h:347-386). */
@@ -136,6 +137,11 @@ int arc_lmhead_argmax(int qtype, const void *w, uint32_t rows, uint32_t K, const
  * thread (bs = super-block quads per row: 1,2,4,8,16; rpl = rows per lane:
  * 1,2,4).  bs = 0 restores the automatic choice. */
 int arc_tune_force(int bs, int rpl);
+
+/* Diagnostic: streaming read of `bytes` (16-byte aligned) with `grid`
+ * workgroups of 256 lanes, 16 bytes per lane access, xor-folded into
+ * out[grid*256] (device).  Measures the practical HBM read ceiling. */
+int arc_probe_read(const void *p, size_t bytes, uint32_t *out, uint32_t grid, arc_stream_t stream);
 
 /* ------------------------------------------------------ synthetic inputs */
 /* Host-side, deterministic generators for seeded synthetic packed tensors

@@ -190,7 +190,7 @@ def test_splitk(qtype, rows, K, splits):
     nb = K // 256
     bps = -(-nb // splits)
     used = -(-nb // bps)
-    gp = part.download(np.float32, used * rows).reshape(used, rows)
+    gp = part.download(np.float32, used * rows).reshape(rows, used).T
     rp = orc.splitk_r64(qtype, w, rows, K, used, x) if used == splits else None
     if rp is not None:
         for j in range(used):
@@ -302,3 +302,41 @@ def test_lmhead_nonfinite_rows_are_skipped_and_counted():
     ref[top] = -np.inf
     ref[5] = -np.inf
     assert tok == int(np.argmax(ref))
+
+
+LAYOUTS = [(1, 1), (1, 2), (2, 1), (2, 2), (4, 1), (4, 2), (8, 1), (8, 2), (16, 1)]
+
+
+@pytest.mark.parametrize("bs,rpl", LAYOUTS)
+def test_every_layout_fused_splitk_lmhead(bs, rpl):
+    """Fused gate/up, one-column-per-split split-K and LM head under each
+    forced lane layout (ragged rows, 14 and 74 super-block columns)."""
+    rows, K = 301, 3584
+    wg = packed(arc.Q4_K, rows, K, 70)
+    wu = packed(arc.Q4_K, rows, K, 71)
+    x = arc.synth_normal(SEED, 72, K)
+    s = arc.DeviceBuffer(rows * 4)
+    dr, dk = 77, 2560  # down-like: 10 columns, one per split
+    wd = packed(arc.Q6_K, dr, dk, 73)
+    xd = arc.synth_normal(SEED, 74, dk)
+    part = arc.DeviceBuffer(10 * dr * 4)
+    yd = arc.DeviceBuffer(dr * 4)
+    wl = packed(arc.Q6_K, rows, K, 75)
+    arc.tune_force(bs, rpl)
+    try:
+        arc.gateup_swiglu(arc.Q4_K, dev(wg), dev(wu), rows, K, dev(x), s)
+        arc.gemv_splitk(arc.Q6_K, dev(wd), dr, dk, 10, dev(xd), part, yd)
+        tok, nf, logits = _lmhead(arc.Q6_K, dev(wl), rows, K, x, None)
+    finally:
+        arc.tune_force(0, 0)
+    g = orc.gemv_r64(arc.Q4_K, wg, rows, K, x)
+    u = orc.gemv_r64(arc.Q4_K, wu, rows, K, x)
+    assert orc.rel_err(s.download(np.float32), orc.swiglu_f64(g, u)) <= TOL
+    rp = orc.splitk_r64(arc.Q6_K, wd, dr, dk, 10, xd)
+    gp = part.download(np.float32).reshape(dr, 10).T
+    for j in range(10):
+        assert orc.rel_err(gp[j], rp[j]) <= TOL
+    assert orc.rel_err(yd.download(np.float32), rp.sum(0)) <= TOL
+    ref = orc.gemv_r64(arc.Q6_K, wl, rows, K, x)
+    assert orc.rel_err(logits, ref) <= TOL
+    assert tok == int(np.argmax(ref)) and nf == 0
