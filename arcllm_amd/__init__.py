@@ -88,6 +88,39 @@ _RESTYPE = {
     "arc_version": C.c_char_p,
     "arc_lmhead_workspace_bytes": C.c_size_t,
 }
+MAX_LAYERS = 64
+T_TOKEN_EMBD, T_OUTPUT, T_OUTPUT_NORM, T_GLOBAL_COUNT = 0, 1, 2, 3
+(T_ATTN_NORM, T_ATTN_Q, T_ATTN_K, T_ATTN_V, T_ATTN_Q_BIAS, T_ATTN_K_BIAS, T_ATTN_V_BIAS, T_ATTN_O,
+ T_FFN_NORM, T_FFN_GATE, T_FFN_UP, T_FFN_DOWN, T_LAYER_COUNT) = range(13)
+DECODE_LOGITS, DECODE_NO_GRAPH = 1, 2
+
+
+class ModelDims(C.Structure):
+    _fields_ = [("hidden", C.c_uint32), ("q_heads", C.c_uint32), ("kv_heads", C.c_uint32),
+                ("head_dim", C.c_uint32), ("ffn", C.c_uint32), ("vocab", C.c_uint32), ("layers", C.c_uint32),
+                ("rms_eps", C.c_float), ("rope_theta", C.c_float),
+                ("v_type", C.c_int32 * MAX_LAYERS), ("down_type", C.c_int32 * MAX_LAYERS)]
+
+
+_SIGS.update({
+    "arc_model_dims_qwen25_7b": [C.POINTER(ModelDims)],
+    "arc_model_tensor_info": [C.POINTER(ModelDims), C.c_int, C.c_int, C.POINTER(C.c_int), C.POINTER(_U32),
+                              C.POINTER(_U32), C.POINTER(_U64)],
+    "arc_model_synth_tensor": [C.POINTER(ModelDims), _U64, C.c_int, C.c_int, _P],
+    "arc_model_create": [C.POINTER(ModelDims), C.POINTER(_P), C.POINTER(_P)],
+    "arc_model_create_synthetic": [C.POINTER(ModelDims), _U64, C.POINTER(_P)],
+    "arc_model_destroy": [_P],
+    "arc_model_weight_bytes": [_P],
+    "arc_session_create": [_P, _U32, C.POINTER(_P)],
+    "arc_session_destroy": [_P],
+    "arc_session_kv": [_P, _U32, C.POINTER(_P), C.POINTER(_P)],
+    "arc_session_fill_kv": [_P, _U32, _U64],
+    "arc_session_decode": [_P, _U32, _U32, _U32, C.c_int, _P, C.POINTER(_U32)],
+    "arc_session_logits": [_P, _P],
+    "arc_session_kernels_per_step": [_P],
+})
+_RESTYPE.update({"arc_model_weight_bytes": _U64, "arc_session_kernels_per_step": _U32})
+
 # Entry points declared in include/*.h that the tests check for.
 EXPORTED = sorted(_SIGS)
 
@@ -292,3 +325,114 @@ def synth_normal(seed: int, stream: int, n: int, mean: float = 0.0, sigma: float
     out = np.empty(n, dtype=np.float32)
     check(lib().arc_synth_normal(seed, stream, n, mean, sigma, out.ctypes.data))
     return out
+
+
+# ------------------------------------------------------------ decode runtime
+def qwen25_7b_dims() -> ModelDims:
+    d = ModelDims()
+    check(lib().arc_model_dims_qwen25_7b(C.byref(d)))
+    return d
+
+
+def tensor_info(dims: ModelDims, layer: int, which: int) -> tuple[int, int, int, int]:
+    """(qtype or 0 for fp32, rows, K, bytes) of a tensor slot (layer -1 for globals)."""
+    qt, rows, K, nb = C.c_int(), C.c_uint32(), C.c_uint32(), C.c_uint64()
+    check(lib().arc_model_tensor_info(C.byref(dims), layer, which, C.byref(qt), C.byref(rows), C.byref(K),
+                                      C.byref(nb)))
+    return qt.value, rows.value, K.value, nb.value
+
+
+def model_slots(dims: ModelDims):
+    """(layer, which) of every tensor slot, in arc_model_create order."""
+    out = [(-1, w) for w in range(T_GLOBAL_COUNT)]
+    for layer in range(dims.layers):
+        out += [(layer, w) for w in range(T_LAYER_COUNT)]
+    return out
+
+
+def synth_model_tensors(dims: ModelDims, seed: int) -> list:
+    """Host arrays of every tensor slot of the random-init model."""
+    arrs = []
+    for layer, which in model_slots(dims):
+        qt, rows, K, nb = tensor_info(dims, layer, which)
+        a = np.empty(nb // 4, np.float32) if qt == 0 else np.empty(nb, np.uint8)
+        check(lib().arc_model_synth_tensor(C.byref(dims), seed, layer, which, a.ctypes.data))
+        arrs.append(a)
+    return arrs
+
+
+class Model:
+    """A model resident in HBM (packed super-blocks copied verbatim)."""
+
+    def __init__(self, dims: ModelDims, tensors=None, seed: int = 0):
+        self.dims = dims
+        h = _P()
+        if tensors is None:
+            check(lib().arc_model_create_synthetic(C.byref(dims), seed, C.byref(h)))
+        else:
+            ptrs = (_P * len(tensors))(*[t.ctypes.data for t in tensors])
+            check(lib().arc_model_create(C.byref(dims), ptrs, C.byref(h)))
+        self.handle = h.value
+
+    @property
+    def weight_bytes(self) -> int:
+        return int(lib().arc_model_weight_bytes(self.handle))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            if _lib is not None:
+                _lib.arc_model_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Session:
+    """fp16 KV cache + working buffers + the captured decode step."""
+
+    def __init__(self, model: Model, max_ctx: int):
+        self.model = model
+        self.max_ctx = max_ctx
+        h = _P()
+        check(lib().arc_session_create(model.handle, max_ctx, C.byref(h)))
+        self.handle = h.value
+
+    def fill_kv(self, ctx: int, seed: int) -> None:
+        check(lib().arc_session_fill_kv(self.handle, ctx, seed))
+
+    def kv(self, layer: int) -> tuple[int, int]:
+        k, v = _P(), _P()
+        check(lib().arc_session_kv(self.handle, layer, C.byref(k), C.byref(v)))
+        return k.value, v.value
+
+    def decode(self, token: int, pos: int, n_steps: int, logits: bool = False, graph: bool = True):
+        out = np.zeros(n_steps, np.uint32)
+        nf = C.c_uint32(0)
+        flags = (DECODE_LOGITS if logits else 0) | (0 if graph else DECODE_NO_GRAPH)
+        check(lib().arc_session_decode(self.handle, token, pos, n_steps, flags, out.ctypes.data, C.byref(nf)))
+        return out, nf.value
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.model.dims.vocab, np.float32)
+        check(lib().arc_session_logits(self.handle, out.ctypes.data))
+        return out
+
+    @property
+    def kernels_per_step(self) -> int:
+        return int(lib().arc_session_kernels_per_step(self.handle))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            if _lib is not None:
+                _lib.arc_session_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,790 @@
+// arc_decode.hip -- the single-token greedy decode step of a Qwen2.5-shaped
+// model on gfx950, and its model/session C ABI (include/arcllm_hip.h).
+//
+// One decode step (src/arcllm_v1_runtime.cpp:371-421 restated as 6 launches
+// per layer instead of 16 dispatches):
+//   embed      token row of token_embd (Q4_K) -> h                      k_embed_q4k
+//   per layer  [attn RMSNorm + q/k GEMV + bias + RoPE + k -> fp16 cache] k_gemv<Q4,EPI_QKROPE>
+//              [attn RMSNorm + v GEMV + bias -> fp16 cache]              k_gemv<v,EPI_VSTORE>
+//              [cached GQA, chunks of 64 positions, fixed-order merge]   k_attn_decode
+//              [o GEMV + residual]                                       k_gemv<Q4,EPI_PLAIN>
+//              [ffn RMSNorm + gate/up GEMV + SwiGLU]                     k_gemv<Q4,EPI_SWIGLU>
+//              [down GEMV + residual]                                    k_gemv<down,EPI_PLAIN>
+//   head       [output RMSNorm + LM head + argmax stage 1]               k_gemv<Q6,EPI_ARGMAX>
+//              [argmax stage 2 -> token, pos += 1]                       k_decode_next
+// The position and token live in a device control block, so the step is
+// captured once as a hipGraph and replayed per token.
+#include "arc_gemv.hpp"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <vector>
+
+namespace arc {
+
+constexpr int kHeadDim = 128;
+constexpr int kChunk = 64;  // positions per attention workgroup
+constexpr int kMaxHpk = 8;  // q heads per kv head
+
+// ----------------------------------------------------------------- kernels
+// h = dequant(token_embd[token]) with the bit-exact element formula.
+__global__ __launch_bounds__(256) void k_embed_q4k(const uint8_t* __restrict__ emb, uint32_t nb,
+                                                   const DecodeCtl* __restrict__ ctl, float* __restrict__ h)
+{
+#pragma clang fp contract(off)
+    const uint32_t token = ctl->token;
+    const uint8_t* row = emb + uint64_t(token) * nb * kQ4Bytes;
+    for (uint32_t e = threadIdx.x; e < nb * kQK; e += 256) {
+        const uint8_t* b = row + (e >> 8) * kQ4Bytes;
+        const uint32_t k = e & 255u, j = k >> 5;
+        const float d = f16_bits_to_f32(uint32_t(b[0]) | (uint32_t(b[1]) << 8));
+        const float dm = f16_bits_to_f32(uint32_t(b[2]) | (uint32_t(b[3]) << 8));
+        const uint8_t* s = b + 4;
+        uint32_t sc, mn;
+        if (j < 4) {
+            sc = s[j] & 63u;
+            mn = s[j + 4] & 63u;
+        } else {
+            sc = (s[j + 4] & 15u) | (uint32_t(s[j - 4] >> 6) << 4);
+            mn = (s[j + 4] >> 4) | (uint32_t(s[j] >> 6) << 4);
+        }
+        const uint32_t l64 = k & 63u;
+        const uint8_t qb = b[16 + (k >> 6) * 32 + (l64 & 31u)];
+        const uint32_t q = l64 < 32u ? (qb & 15u) : (qb >> 4);
+        const float t0 = d * float(sc);
+        const float t1 = t0 * float(q);
+        const float t2 = dm * float(mn);
+        h[e] = t1 - t2;
+    }
+}
+
+struct AttnParams {
+    const float* q;           // [q_heads*128], RoPE applied
+    const _Float16* kc;       // this layer's K cache [max_ctx][kv_heads*128]
+    const _Float16* vc;       // this layer's V cache
+    float* out;               // [q_heads*128]
+    float* part;              // [kv_heads][max_chunks][hpk][2 + 128]: m, l, o
+    uint32_t* counters;       // [kv_heads], zero between launches
+    const DecodeCtl* ctl;
+    uint32_t kv_heads, hpk, max_chunks;
+    float scale;
+};
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+// Cached GQA for one new position (flash-decoding).  Workgroup (c, g) covers
+// positions [64c, 64c+64) of kv head g for its hpk query heads: scores, a
+// chunk-local softmax (max m, sum l) and the weighted V sum o.  The last
+// workgroup of kv head g to finish (atomic ticket) merges the chunks in
+// chunk order: out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).
+// Semantics: src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1177-1212,
+// shaders/p7_attention_kv_online.comp (kv head = q head / (q_heads/kv_heads)).
+__global__ __launch_bounds__(256) void k_attn_decode(AttnParams a)
+{
+    const uint32_t T = a.ctl->pos + 1;
+    const uint32_t nch = (T + kChunk - 1) / kChunk;
+    const uint32_t c = blockIdx.x, g = blockIdx.y;
+    if (c >= nch) return;
+    const uint32_t t0 = c * kChunk, nt = min(uint32_t(kChunk), T - t0);
+    const uint32_t hpk = a.hpk, kvd = a.kv_heads * kHeadDim;
+    const int tid = threadIdx.x;
+
+    __shared__ float qs[kMaxHpk][kHeadDim];
+    __shared__ float sc[kMaxHpk][kChunk];
+    __shared__ float ored[4][kMaxHpk][kHeadDim];
+    __shared__ float mh[kMaxHpk], lh[kMaxHpk];
+    __shared__ uint32_t last;
+
+    for (uint32_t i = tid; i < hpk * kHeadDim; i += 256) qs[i >> 7][i & 127u] = a.q[g * hpk * kHeadDim + i];
+    __syncthreads();
+
+    {   // scores: thread -> position tid/4, dims (tid%4)*32 .. +32
+        const uint32_t t = uint32_t(tid) >> 2, part = tid & 3;
+        float s[kMaxHpk];
+#pragma unroll
+        for (int h = 0; h < kMaxHpk; ++h) s[h] = 0.0f;
+        if (t < nt) {
+            const uint4* kp = reinterpret_cast<const uint4*>(a.kc + uint64_t(t0 + t) * kvd + g * kHeadDim + part * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint4 raw = kp[i];
+                const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float kv = static_cast<float>(__builtin_bit_cast(half2_t, w4[e >> 1])[e & 1]);
+                    const int d = part * 32 + i * 8 + e;
+#pragma unroll
+                    for (int h = 0; h < kMaxHpk; ++h)
+                        if (uint32_t(h) < hpk) s[h] = __builtin_fmaf(qs[h][d], kv, s[h]);
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < kMaxHpk; ++h) s[h] = group_sum<4>(s[h]);
+        if (part == 0 && t < nt)
+#pragma unroll
+            for (int h = 0; h < kMaxHpk; ++h)
+                if (uint32_t(h) < hpk) sc[h][t] = s[h] * a.scale;
+    }
+    __syncthreads();
+
+    {   // chunk softmax: wave w handles heads w and w+4
+        const int w = tid >> 6, lane = tid & 63;
+        for (uint32_t h = w; h < hpk; h += 4) {
+            const float s = uint32_t(lane) < nt ? sc[h][lane] : -INFINITY;
+            const float m = wave_max(s);
+            const float e = uint32_t(lane) < nt ? expf(s - m) : 0.0f;
+            const float l = group_sum<kWave>(e);
+            sc[h][lane] = e;
+            if (lane == 0) {
+                mh[h] = m;
+                lh[h] = l;
+            }
+        }
+    }
+    __syncthreads();
+
+    {   // weighted V: thread -> dims 2i, 2i+1 and positions 16*pg .. +16
+        const int i = tid & 63, pg = tid >> 6;
+        float o[kMaxHpk][2];
+#pragma unroll
+        for (int h = 0; h < kMaxHpk; ++h) o[h][0] = o[h][1] = 0.0f;
+        for (int tt = 0; tt < 16; ++tt) {
+            const uint32_t t = pg * 16 + tt;
+            if (t >= nt) break;
+            const half2_t vv =
+                *reinterpret_cast<const half2_t*>(a.vc + uint64_t(t0 + t) * kvd + g * kHeadDim + 2 * i);
+            const float v0 = static_cast<float>(vv.x), v1 = static_cast<float>(vv.y);
+#pragma unroll
+            for (int h = 0; h < kMaxHpk; ++h) {
+                if (uint32_t(h) < hpk) {
+                    const float p = sc[h][t];
+                    o[h][0] = __builtin_fmaf(p, v0, o[h][0]);
+                    o[h][1] = __builtin_fmaf(p, v1, o[h][1]);
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < kMaxHpk; ++h) {
+            ored[pg][h][2 * i] = o[h][0];
+            ored[pg][h][2 * i + 1] = o[h][1];
+        }
+    }
+    __syncthreads();
+
+    float* pbase = a.part + (uint64_t(g) * a.max_chunks + c) * hpk * (2 + kHeadDim);
+    for (uint32_t idx = tid; idx < hpk * kHeadDim; idx += 256) {
+        const uint32_t h = idx >> 7, d = idx & 127u;
+        pbase[h * (2 + kHeadDim) + 2 + d] = ((ored[0][h][d] + ored[1][h][d]) + ored[2][h][d]) + ored[3][h][d];
+    }
+    if (uint32_t(tid) < hpk) {
+        pbase[tid * (2 + kHeadDim)] = mh[tid];
+        pbase[tid * (2 + kHeadDim) + 1] = lh[tid];
+    }
+
+    // the last workgroup of this kv head merges all chunks, in chunk order
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last = (atomicAdd(&a.counters[g], 1u) == nch - 1) ? 1u : 0u;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+
+    __shared__ float Mh[kMaxHpk], Lh[kMaxHpk];
+    const float* gbase = a.part + uint64_t(g) * a.max_chunks * hpk * (2 + kHeadDim);
+    auto ld = [](const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    if (uint32_t(tid) < hpk) {
+        float M = -INFINITY;
+        for (uint32_t cc = 0; cc < nch; ++cc) M = fmaxf(M, ld(gbase + (cc * hpk + tid) * (2 + kHeadDim)));
+        float L = 0.0f;
+        for (uint32_t cc = 0; cc < nch; ++cc) {
+            const float* pc = gbase + (cc * hpk + tid) * (2 + kHeadDim);
+            L += ld(pc + 1) * expf(ld(pc) - M);
+        }
+        Mh[tid] = M;
+        Lh[tid] = L;
+    }
+    __syncthreads();
+    for (uint32_t idx = tid; idx < hpk * kHeadDim; idx += 256) {
+        const uint32_t h = idx >> 7, d = idx & 127u;
+        float acc = 0.0f;
+        for (uint32_t cc = 0; cc < nch; ++cc) {
+            const float* pc = gbase + (cc * hpk + h) * (2 + kHeadDim);
+            acc += ld(pc + 2 + d) * expf(ld(pc) - Mh[h]);
+        }
+        a.out[(g * hpk + h) * kHeadDim + d] = acc / Lh[h];
+    }
+    if (tid == 0) a.counters[g] = 0u;
+}
+
+// Argmax stage 2 of a decode step: token = argmax, recorded at out[step];
+// the control block advances to the next position.
+__global__ __launch_bounds__(1024) void k_decode_next(const ArgBest* __restrict__ best, uint32_t n,
+                                                      DecodeCtl* __restrict__ ctl, uint32_t* __restrict__ out,
+                                                      uint32_t out_cap)
+{
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu, nf = 0;
+    for (uint32_t i0 = 0; i0 < n; i0 += 4096u) {
+        ArgBest b[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t i = i0 + k * 1024u + threadIdx.x;
+            b[k] = i < n ? best[i] : ArgBest{-INFINITY, 0xffffffffu, 0u, 0u};
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (b[k].idx != 0xffffffffu && arg_better(b[k].val, b[k].idx, bv, bi)) {
+                bv = b[k].val;
+                bi = b[k].idx;
+            }
+            nf += b[k].nonfinite;
+        }
+    }
+    __shared__ ArgBest res;
+    wg_argmax(bv, bi, nf, &res);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t tok = (res.idx == 0xffffffffu) ? 0u : res.idx;
+        const uint32_t step = ctl->step;
+        if (step < out_cap) out[step] = tok;
+        ctl->token = tok;
+        ctl->nonfinite += res.nonfinite;
+        ctl->step = step + 1;
+        ctl->pos += 1;
+    }
+}
+
+// ------------------------------------------------------------ host objects
+struct Layer {
+    const uint8_t *q, *k, *v, *o, *gate, *up, *down;
+    const float *attn_norm, *ffn_norm, *qb, *kb, *vb;
+    int v_type, down_type;
+};
+
+}  // namespace arc
+
+struct arc_model {
+    arc_model_dims dims{};
+    std::vector<void*> allocations;  // device memory owned by the model
+    const uint8_t* emb = nullptr;
+    const uint8_t* out = nullptr;
+    const float* out_norm = nullptr;
+    std::vector<arc::Layer> layers;
+    uint64_t weight_bytes = 0;
+
+    ~arc_model()
+    {
+        for (void* p : allocations) (void)hipFree(p);
+    }
+};
+
+struct arc_session {
+    arc_model* model = nullptr;
+    uint32_t max_ctx = 0;
+    uint32_t max_chunks = 0;
+    hipStream_t stream = nullptr;
+    std::vector<void*> allocations;
+    _Float16* kcache = nullptr;  // [layers][max_ctx][kv_dim]
+    _Float16* vcache = nullptr;
+    float *h = nullptr, *h1 = nullptr, *q = nullptr, *attn = nullptr, *s = nullptr, *logits = nullptr;
+    float* apart = nullptr;
+    uint32_t* counters = nullptr;
+    double* inv_freq = nullptr;
+    arc::ArgBest* best = nullptr;
+    uint32_t best_cap = 0;
+    arc::DecodeCtl* ctl = nullptr;
+    uint32_t* out_tokens = nullptr;
+    uint32_t out_cap = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    bool graph_logits = false;
+    uint32_t kernels_per_step = 0;
+
+    ~arc_session()
+    {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (stream) (void)hipStreamDestroy(stream);
+        for (void* p : allocations) (void)hipFree(p);
+    }
+};
+
+namespace arc {
+
+static uint64_t packed_bytes(int qtype, uint32_t rows, uint32_t K)
+{
+    return uint64_t(rows) * (K / kQK) * (qtype == kFmtQ4 ? kQ4Bytes : kQ6Bytes);
+}
+
+static int dims_ok(const arc_model_dims& d)
+{
+    if (d.hidden == 0 || d.hidden % kQK || d.ffn == 0 || d.ffn % kQK || d.head_dim != kHeadDim || d.q_heads == 0 ||
+        d.kv_heads == 0 || d.q_heads % d.kv_heads || d.q_heads / d.kv_heads > kMaxHpk ||
+        d.q_heads * kHeadDim != d.hidden || d.vocab == 0 || d.layers == 0 || d.layers > ARC_MAX_LAYERS)
+        return set_error(ARC_ERR_UNSUPPORTED,
+                         "unsupported model dims (hidden %u, heads %u/%u, head_dim %u, ffn %u, vocab %u, layers %u)",
+                         d.hidden, d.q_heads, d.kv_heads, d.head_dim, d.ffn, d.vocab, d.layers);
+    if (d.hidden / kQK > uint32_t(kPanel) || d.ffn / kQK > uint32_t(kPanel))
+        return set_error(ARC_ERR_UNSUPPORTED, "hidden and ffn must be <= %d", kPanel * kQK);
+    for (uint32_t l = 0; l < d.layers; ++l)
+        if ((d.v_type[l] != kFmtQ4 && d.v_type[l] != kFmtQ6) || (d.down_type[l] != kFmtQ4 && d.down_type[l] != kFmtQ6))
+            return set_error(ARC_ERR_UNSUPPORTED, "layer %u: attn_v / ffn_down must be Q4_K or Q6_K", l);
+    return ARC_OK;
+}
+
+// Launch one decode step on the session stream (captured into a graph by the
+// caller, or run eagerly).  Returns the number of kernels launched.
+static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
+{
+    arc_model* M = S->model;
+    const arc_model_dims& d = M->dims;
+    hipStream_t st = S->stream;
+    const uint32_t H = d.hidden, KVD = d.kv_heads * kHeadDim, F = d.ffn;
+    uint32_t n = 0;
+    auto chk = [&](hipError_t e, const char* what) { ++n; return check_hip(e, what); };
+
+    if (!g_dry_run) hipLaunchKernelGGL(k_embed_q4k, dim3(1), dim3(256), 0, st, M->emb, H / kQK, S->ctl, S->h);
+    int rc = chk(hipGetLastError(), "embed");
+    if (rc) return rc;
+
+    for (uint32_t l = 0; l < d.layers; ++l) {
+        const Layer& L = M->layers[l];
+        _Float16* kc = S->kcache + uint64_t(l) * S->max_ctx * KVD;
+        _Float16* vc = S->vcache + uint64_t(l) * S->max_ctx * KVD;
+
+        // q/k projection + RoPE + K store
+        GemvParams p = make_params(kFmtQ4, L.q, L.k, H + KVD, H, S->h);
+        p.flags = F_NORM;
+        p.normw = L.attn_norm;
+        p.eps = d.rms_eps;
+        p.bias = L.qb;
+        p.bias2 = L.kb;
+        p.row_split = H;
+        p.kv_dim = KVD;
+        p.cache = kc;
+        p.inv_freq = S->inv_freq;
+        p.ctl = S->ctl;
+        p.y = S->q;
+        if ((rc = chk(launch_one<kFmtQ4, EPI_QKROPE, 16, 2>(p, 1, st, nullptr), "q/k projection"))) return rc;
+
+        // v projection + V store
+        p = make_params(L.v_type, L.v, nullptr, KVD, H, S->h);
+        p.flags = F_NORM;
+        p.normw = L.attn_norm;
+        p.eps = d.rms_eps;
+        p.bias = L.vb;
+        p.kv_dim = KVD;
+        p.cache = vc;
+        p.ctl = S->ctl;
+        hipError_t e = L.v_type == kFmtQ4 ? launch_one<kFmtQ4, EPI_VSTORE, 16, 1>(p, 1, st, nullptr)
+                                          : launch_one<kFmtQ6, EPI_VSTORE, 16, 1>(p, 1, st, nullptr);
+        if ((rc = chk(e, "v projection"))) return rc;
+
+        // attention
+        AttnParams ap{};
+        ap.q = S->q;
+        ap.kc = kc;
+        ap.vc = vc;
+        ap.out = S->attn;
+        ap.part = S->apart;
+        ap.counters = S->counters;
+        ap.ctl = S->ctl;
+        ap.kv_heads = d.kv_heads;
+        ap.hpk = d.q_heads / d.kv_heads;
+        ap.max_chunks = S->max_chunks;
+        ap.scale = 1.0f / std::sqrt(float(kHeadDim));
+        if (!g_dry_run) hipLaunchKernelGGL(k_attn_decode, dim3(S->max_chunks, d.kv_heads), dim3(256), 0, st, ap);
+        if ((rc = chk(hipGetLastError(), "attention"))) return rc;
+
+        // o projection + residual: h1 = h + Wo attn
+        p = make_params(kFmtQ4, L.o, nullptr, H, H, S->attn);
+        p.res = S->h;
+        p.y = S->h1;
+        if ((rc = chk(launch_gemv_epi(EPI_PLAIN, kFmtQ4, choose_cfg(EPI_PLAIN, H, H / kQK, 1), p, 1, st), "o projection")))
+            return rc;
+
+        // ffn RMSNorm + gate/up + SwiGLU
+        p = make_params(kFmtQ4, L.gate, L.up, F, H, S->h1);
+        p.flags = F_NORM;
+        p.normw = L.ffn_norm;
+        p.eps = d.rms_eps;
+        p.y = S->s;
+        if ((rc = chk(launch_gemv_epi(EPI_SWIGLU, kFmtQ4, choose_cfg(EPI_SWIGLU, F, H / kQK, 1), p, 1, st), "gate/up")))
+            return rc;
+
+        // down + residual: h = h1 + Wd s
+        p = make_params(L.down_type, L.down, nullptr, H, F, S->s);
+        p.res = S->h1;
+        p.y = S->h;
+        if ((rc = chk(launch_gemv_epi(EPI_PLAIN, L.down_type, choose_cfg(EPI_PLAIN, H, F / kQK, 1), p, 1, st),
+                      "down projection")))
+            return rc;
+    }
+
+    // output RMSNorm + LM head + argmax
+    GemvParams p = make_params(kFmtQ6, M->out, nullptr, d.vocab, H, S->h);
+    p.flags = F_NORM;
+    p.normw = M->out_norm;
+    p.eps = d.rms_eps;
+    p.y = logits ? S->logits : nullptr;
+    p.best = S->best;
+    uint32_t gx = 0;
+    if ((rc = chk(launch_gemv_epi(EPI_ARGMAX, kFmtQ6, choose_cfg(EPI_ARGMAX, d.vocab, H / kQK, 1), p, 1, st, &gx),
+                  "lm head")))
+        return rc;
+    if (gx > S->best_cap) return set_error(ARC_ERR_UNSUPPORTED, "internal: argmax grid %u > %u", gx, S->best_cap);
+    if (!g_dry_run)
+        hipLaunchKernelGGL(k_decode_next, dim3(1), dim3(1024), 0, st, S->best, gx, S->ctl, S->out_tokens, S->out_cap);
+    if ((rc = chk(hipGetLastError(), "argmax"))) return rc;
+    if (nkernels) *nkernels = n;
+    return ARC_OK;
+}
+
+}  // namespace arc
+
+using namespace arc;
+
+extern "C" {
+
+int arc_model_dims_qwen25_7b(arc_model_dims* d)
+{
+    if (!d) return set_error(ARC_ERR_INVALID_ARGUMENT, "null dims");
+    std::memset(d, 0, sizeof(*d));
+    d->hidden = 3584;
+    d->q_heads = 28;
+    d->kv_heads = 4;
+    d->head_dim = 128;
+    d->ffn = 18944;
+    d->vocab = 152064;
+    d->layers = 28;
+    d->rms_eps = 1e-6f;
+    d->rope_theta = 1e6f;
+    for (uint32_t l = 0; l < ARC_MAX_LAYERS; ++l) {
+        d->v_type[l] = ARC_Q6_K;
+        d->down_type[l] = ARC_Q6_K;
+    }
+    return ARC_OK;
+}
+
+int arc_model_tensor_info(const arc_model_dims* d, int layer, int which, int* qtype, uint32_t* rows, uint32_t* K,
+                          uint64_t* bytes)
+{
+    if (!d || !qtype || !rows || !K || !bytes) return set_error(ARC_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = dims_ok(*d);
+    if (rc) return rc;
+    const uint32_t H = d->hidden, KVD = d->kv_heads * kHeadDim;
+    int t = 0;
+    uint32_t r = 0, k = 0;
+    if (layer < 0) {
+        switch (which) {
+        case ARC_T_TOKEN_EMBD: t = ARC_Q4_K, r = d->vocab, k = H; break;
+        case ARC_T_OUTPUT: t = ARC_Q6_K, r = d->vocab, k = H; break;
+        case ARC_T_OUTPUT_NORM: t = 0, r = 1, k = H; break;
+        default: return set_error(ARC_ERR_INVALID_ARGUMENT, "bad global tensor %d", which);
+        }
+    } else {
+        if (uint32_t(layer) >= d->layers) return set_error(ARC_ERR_INVALID_ARGUMENT, "layer %d out of range", layer);
+        switch (which) {
+        case ARC_T_ATTN_NORM: case ARC_T_FFN_NORM: t = 0, r = 1, k = H; break;
+        case ARC_T_ATTN_Q: case ARC_T_ATTN_O: t = ARC_Q4_K, r = H, k = H; break;
+        case ARC_T_ATTN_K: t = ARC_Q4_K, r = KVD, k = H; break;
+        case ARC_T_ATTN_V: t = d->v_type[layer], r = KVD, k = H; break;
+        case ARC_T_ATTN_Q_BIAS: t = 0, r = 1, k = H; break;
+        case ARC_T_ATTN_K_BIAS: case ARC_T_ATTN_V_BIAS: t = 0, r = 1, k = KVD; break;
+        case ARC_T_FFN_GATE: case ARC_T_FFN_UP: t = ARC_Q4_K, r = d->ffn, k = H; break;
+        case ARC_T_FFN_DOWN: t = d->down_type[layer], r = H, k = d->ffn; break;
+        default: return set_error(ARC_ERR_INVALID_ARGUMENT, "bad layer tensor %d", which);
+        }
+    }
+    *qtype = t;
+    *rows = r;
+    *K = k;
+    *bytes = t == 0 ? uint64_t(k) * 4 : packed_bytes(t, r, k);
+    return ARC_OK;
+}
+
+int arc_model_synth_tensor(const arc_model_dims* d, uint64_t seed, int layer, int which, void* out)
+{
+    int qtype;
+    uint32_t rows, K;
+    uint64_t bytes;
+    int rc = arc_model_tensor_info(d, layer, which, &qtype, &rows, &K, &bytes);
+    if (rc) return rc;
+    const uint64_t stream = layer < 0 ? uint64_t(which) : 100ull + 16ull * uint64_t(layer) + uint64_t(which);
+    // zero-mean, small-scale init: E[d*sc*q] = E[dmin*mn] for Q4_K, so rows
+    // are centred and activations stay O(1) through the layers
+    if (qtype != 0) return arc_synth_packed(qtype, seed, stream, rows, K, 1e-4f, 7.5e-4f, out);
+    const bool norm = which == ARC_T_OUTPUT_NORM || which == ARC_T_ATTN_NORM || which == ARC_T_FFN_NORM;
+    return arc_synth_normal(seed, stream, K, norm ? 1.0f : 0.0f, norm ? 0.05f : 0.1f, static_cast<float*>(out));
+}
+
+int arc_model_create(const arc_model_dims* dims, const void* const* tensors, arc_model** out)
+{
+    if (!dims || !tensors || !out) return set_error(ARC_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    int rc = dims_ok(*dims);
+    if (rc) return rc;
+    std::unique_ptr<arc_model> M(new (std::nothrow) arc_model);
+    if (!M) return set_error(ARC_ERR_OUT_OF_MEMORY, "host allocation");
+    M->dims = *dims;
+    auto upload = [&](int layer, int which, const void** dst) -> int {
+        int qtype;
+        uint32_t rows, K;
+        uint64_t bytes;
+        int r = arc_model_tensor_info(dims, layer, which, &qtype, &rows, &K, &bytes);
+        if (r) return r;
+        const size_t idx = layer < 0 ? size_t(which) : size_t(ARC_T_GLOBAL_COUNT) + size_t(layer) * ARC_T_LAYER_COUNT + which;
+        const void* src = tensors[idx];
+        if (!src) return set_error(ARC_ERR_INVALID_ARGUMENT, "tensor %zu is null", idx);
+        void* p = nullptr;
+        if ((r = check_hip(hipMalloc(&p, bytes + 256), "hipMalloc weights"))) return r;  // slack: 16 B loads
+        M->allocations.push_back(p);
+        if ((r = check_hip(hipMemcpy(p, src, bytes, hipMemcpyHostToDevice), "upload weights"))) return r;
+        M->weight_bytes += bytes;
+        *dst = p;
+        return ARC_OK;
+    };
+    const void* tmp = nullptr;
+    if ((rc = upload(-1, ARC_T_TOKEN_EMBD, &tmp))) return rc;
+    M->emb = static_cast<const uint8_t*>(tmp);
+    if ((rc = upload(-1, ARC_T_OUTPUT, &tmp))) return rc;
+    M->out = static_cast<const uint8_t*>(tmp);
+    if ((rc = upload(-1, ARC_T_OUTPUT_NORM, &tmp))) return rc;
+    M->out_norm = static_cast<const float*>(tmp);
+    M->layers.resize(dims->layers);
+    for (uint32_t l = 0; l < dims->layers; ++l) {
+        Layer& L = M->layers[l];
+        const void* t[ARC_T_LAYER_COUNT] = {};
+        for (int w = 0; w < ARC_T_LAYER_COUNT; ++w)
+            if ((rc = upload(int(l), w, &t[w]))) return rc;
+        L.attn_norm = static_cast<const float*>(t[ARC_T_ATTN_NORM]);
+        L.q = static_cast<const uint8_t*>(t[ARC_T_ATTN_Q]);
+        L.k = static_cast<const uint8_t*>(t[ARC_T_ATTN_K]);
+        L.v = static_cast<const uint8_t*>(t[ARC_T_ATTN_V]);
+        L.qb = static_cast<const float*>(t[ARC_T_ATTN_Q_BIAS]);
+        L.kb = static_cast<const float*>(t[ARC_T_ATTN_K_BIAS]);
+        L.vb = static_cast<const float*>(t[ARC_T_ATTN_V_BIAS]);
+        L.o = static_cast<const uint8_t*>(t[ARC_T_ATTN_O]);
+        L.ffn_norm = static_cast<const float*>(t[ARC_T_FFN_NORM]);
+        L.gate = static_cast<const uint8_t*>(t[ARC_T_FFN_GATE]);
+        L.up = static_cast<const uint8_t*>(t[ARC_T_FFN_UP]);
+        L.down = static_cast<const uint8_t*>(t[ARC_T_FFN_DOWN]);
+        L.v_type = dims->v_type[l];
+        L.down_type = dims->down_type[l];
+    }
+    *out = M.release();
+    return ARC_OK;
+}
+
+int arc_model_create_synthetic(const arc_model_dims* dims, uint64_t seed, arc_model** out)
+{
+    if (!dims || !out) return set_error(ARC_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = dims_ok(*dims);
+    if (rc) return rc;
+    const size_t nt = size_t(ARC_T_GLOBAL_COUNT) + size_t(dims->layers) * ARC_T_LAYER_COUNT;
+    std::vector<std::vector<uint8_t>> host(nt);
+    std::vector<const void*> ptrs(nt, nullptr);
+    // generate and upload tensor by tensor to bound host memory
+    std::unique_ptr<arc_model> dummy;
+    for (size_t i = 0; i < nt; ++i) {
+        const int layer = i < size_t(ARC_T_GLOBAL_COUNT) ? -1 : int((i - ARC_T_GLOBAL_COUNT) / ARC_T_LAYER_COUNT);
+        const int which = i < size_t(ARC_T_GLOBAL_COUNT) ? int(i) : int((i - ARC_T_GLOBAL_COUNT) % ARC_T_LAYER_COUNT);
+        int qtype;
+        uint32_t rows, K;
+        uint64_t bytes;
+        if ((rc = arc_model_tensor_info(dims, layer, which, &qtype, &rows, &K, &bytes))) return rc;
+        host[i].resize(bytes);
+        if ((rc = arc_model_synth_tensor(dims, seed, layer, which, host[i].data()))) return rc;
+        ptrs[i] = host[i].data();
+    }
+    return arc_model_create(dims, ptrs.data(), out);
+}
+
+int arc_model_destroy(arc_model* m)
+{
+    delete m;
+    return ARC_OK;
+}
+
+uint64_t arc_model_weight_bytes(const arc_model* m) { return m ? m->weight_bytes : 0; }
+
+int arc_session_create(arc_model* m, uint32_t max_ctx, arc_session** out)
+{
+    if (!m || !out || max_ctx == 0) return set_error(ARC_ERR_INVALID_ARGUMENT, "bad session arguments");
+    *out = nullptr;
+    std::unique_ptr<arc_session> S(new (std::nothrow) arc_session);
+    if (!S) return set_error(ARC_ERR_OUT_OF_MEMORY, "host allocation");
+    const arc_model_dims& d = m->dims;
+    S->model = m;
+    S->max_ctx = max_ctx;
+    S->max_chunks = (max_ctx + kChunk - 1) / kChunk;
+    S->out_cap = max_ctx;
+    const uint32_t KVD = d.kv_heads * kHeadDim, H = d.hidden;
+    int rc = check_hip(hipStreamCreateWithFlags(&S->stream, hipStreamNonBlocking), "stream");
+    if (rc) return rc;
+    auto alloc = [&](void** p, size_t bytes) {
+        int r = check_hip(hipMalloc(p, bytes), "hipMalloc session");
+        if (!r) S->allocations.push_back(*p);
+        return r;
+    };
+    const uint64_t kv = uint64_t(d.layers) * max_ctx * KVD * sizeof(_Float16);
+    S->best_cap = min((d.vocab + 3u) / 4u, 65536u);
+    void* p = nullptr;
+    if ((rc = alloc(&p, kv))) return rc;
+    S->kcache = static_cast<_Float16*>(p);
+    if ((rc = alloc(&p, kv))) return rc;
+    S->vcache = static_cast<_Float16*>(p);
+    const size_t fl = sizeof(float);
+    if ((rc = alloc(&p, H * fl))) return rc;
+    S->h = static_cast<float*>(p);
+    if ((rc = alloc(&p, H * fl))) return rc;
+    S->h1 = static_cast<float*>(p);
+    if ((rc = alloc(&p, H * fl))) return rc;
+    S->q = static_cast<float*>(p);
+    if ((rc = alloc(&p, H * fl))) return rc;
+    S->attn = static_cast<float*>(p);
+    if ((rc = alloc(&p, size_t(d.ffn) * fl))) return rc;
+    S->s = static_cast<float*>(p);
+    if ((rc = alloc(&p, size_t(d.vocab) * fl))) return rc;
+    S->logits = static_cast<float*>(p);
+    if ((rc = alloc(&p, size_t(d.kv_heads) * S->max_chunks * (d.q_heads / d.kv_heads) * (2 + kHeadDim) * fl))) return rc;
+    S->apart = static_cast<float*>(p);
+    if ((rc = alloc(&p, d.kv_heads * sizeof(uint32_t)))) return rc;
+    S->counters = static_cast<uint32_t*>(p);
+    if ((rc = alloc(&p, 64 * sizeof(double)))) return rc;
+    S->inv_freq = static_cast<double*>(p);
+    if ((rc = alloc(&p, size_t(S->best_cap) * sizeof(ArgBest)))) return rc;
+    S->best = static_cast<ArgBest*>(p);
+    if ((rc = alloc(&p, sizeof(DecodeCtl)))) return rc;
+    S->ctl = static_cast<DecodeCtl*>(p);
+    if ((rc = alloc(&p, size_t(S->out_cap) * sizeof(uint32_t)))) return rc;
+    S->out_tokens = static_cast<uint32_t*>(p);
+    double inv[64];
+    for (int i = 0; i < 64; ++i) inv[i] = std::pow(double(d.rope_theta), -2.0 * double(i) / double(kHeadDim));
+    if ((rc = check_hip(hipMemcpy(S->inv_freq, inv, sizeof(inv), hipMemcpyHostToDevice), "inv_freq"))) return rc;
+    if ((rc = check_hip(hipMemset(S->counters, 0, d.kv_heads * sizeof(uint32_t)), "counters"))) return rc;
+    if ((rc = check_hip(hipMemset(S->kcache, 0, kv), "kcache"))) return rc;
+    if ((rc = check_hip(hipMemset(S->vcache, 0, kv), "vcache"))) return rc;
+    *out = S.release();
+    return ARC_OK;
+}
+
+int arc_session_destroy(arc_session* s)
+{
+    delete s;
+    return ARC_OK;
+}
+
+int arc_session_kv(arc_session* s, uint32_t layer, void** k, void** v)
+{
+    if (!s || !k || !v || layer >= s->model->dims.layers) return set_error(ARC_ERR_INVALID_ARGUMENT, "bad kv query");
+    const uint64_t off = uint64_t(layer) * s->max_ctx * s->model->dims.kv_heads * kHeadDim;
+    *k = s->kcache + off;
+    *v = s->vcache + off;
+    return ARC_OK;
+}
+
+int arc_session_fill_kv(arc_session* s, uint32_t ctx, uint64_t seed)
+{
+    if (!s || ctx > s->max_ctx) return set_error(ARC_ERR_INVALID_ARGUMENT, "bad kv fill");
+    const arc_model_dims& d = s->model->dims;
+    const size_t row = size_t(d.kv_heads) * kHeadDim, n = size_t(ctx) * row;
+    std::vector<float> f(n);
+    std::vector<_Float16> hbuf(n);
+    for (uint32_t l = 0; l < d.layers; ++l) {
+        for (int kv = 0; kv < 2; ++kv) {
+            int rc = arc_synth_normal(seed, 1000000ull + 2ull * l + uint64_t(kv), n, 0.0f, 1.0f, f.data());
+            if (rc) return rc;
+            for (size_t i = 0; i < n; ++i) hbuf[i] = static_cast<_Float16>(f[i]);
+            _Float16* dst = (kv ? s->vcache : s->kcache) + uint64_t(l) * s->max_ctx * row;
+            if ((rc = check_hip(hipMemcpy(dst, hbuf.data(), n * sizeof(_Float16), hipMemcpyHostToDevice), "kv fill")))
+                return rc;
+        }
+    }
+    return ARC_OK;
+}
+
+int arc_session_decode(arc_session* s, uint32_t token, uint32_t pos, uint32_t n_steps, int flags, uint32_t* out_tokens,
+                       uint32_t* nonfinite)
+{
+    if (!s || n_steps == 0) return set_error(ARC_ERR_INVALID_ARGUMENT, "bad decode arguments");
+    const arc_model_dims& d = s->model->dims;
+    if (token >= d.vocab) return set_error(ARC_ERR_INVALID_ARGUMENT, "token %u out of vocabulary", token);
+    if (uint64_t(pos) + n_steps > s->max_ctx)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "positions %u..%u exceed the context %u", pos, pos + n_steps - 1,
+                         s->max_ctx);
+    const bool logits = (flags & ARC_DECODE_LOGITS) != 0;
+    const bool use_graph = (flags & ARC_DECODE_NO_GRAPH) == 0;
+    DecodeCtl c{pos, token, 0u, 0u};
+    int rc = check_hip(hipMemcpyAsync(s->ctl, &c, sizeof(c), hipMemcpyHostToDevice, s->stream), "ctl upload");
+    if (rc) return rc;
+    if (use_graph && (!s->exec || s->graph_logits != logits)) {
+        if (s->exec) {
+            (void)hipGraphExecDestroy(s->exec);
+            (void)hipGraphDestroy(s->graph);
+            s->exec = nullptr;
+            s->graph = nullptr;
+        }
+        // a dry run fills the launch helpers' occupancy caches (host-side
+        // queries) before the capture starts
+        g_dry_run = true;
+        rc = launch_step(s, logits, nullptr);
+        g_dry_run = false;
+        if (rc) return rc;
+        if ((rc = check_hip(hipStreamSynchronize(s->stream), "sync"))) return rc;
+        if ((rc = check_hip(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal), "begin capture")))
+            return rc;
+        uint32_t nk = 0;
+        rc = launch_step(s, logits, &nk);
+        hipGraph_t g = nullptr;
+        const int rc2 = check_hip(hipStreamEndCapture(s->stream, &g), "end capture");
+        if (rc) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        if (rc2) return rc2;
+        s->graph = g;
+        if ((rc = check_hip(hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0), "instantiate"))) return rc;
+        s->graph_logits = logits;
+        s->kernels_per_step = nk;
+    }
+    for (uint32_t i = 0; i < n_steps; ++i) {
+        if (use_graph) {
+            if ((rc = check_hip(hipGraphLaunch(s->exec, s->stream), "graph launch"))) return rc;
+        } else {
+            uint32_t nk = 0;
+            if ((rc = launch_step(s, logits, &nk))) return rc;
+            s->kernels_per_step = nk;
+        }
+    }
+    if (out_tokens && (rc = check_hip(hipMemcpyAsync(out_tokens, s->out_tokens, n_steps * sizeof(uint32_t),
+                                                     hipMemcpyDeviceToHost, s->stream),
+                                      "tokens download")))
+        return rc;
+    DecodeCtl after{};
+    if ((rc = check_hip(hipMemcpyAsync(&after, s->ctl, sizeof(after), hipMemcpyDeviceToHost, s->stream), "ctl")))
+        return rc;
+    if ((rc = check_hip(hipStreamSynchronize(s->stream), "decode sync"))) return rc;
+    if (nonfinite) *nonfinite = after.nonfinite;
+    return ARC_OK;
+}
+
+int arc_session_logits(arc_session* s, float* host_logits)
+{
+    if (!s || !host_logits) return set_error(ARC_ERR_INVALID_ARGUMENT, "bad logits query");
+    return check_hip(hipMemcpy(host_logits, s->logits, size_t(s->model->dims.vocab) * sizeof(float), hipMemcpyDeviceToHost),
+                     "logits download");
+}
+
+uint32_t arc_session_kernels_per_step(const arc_session* s) { return s ? s->kernels_per_step : 0; }
+
+}  // extern "C"

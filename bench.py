@@ -100,6 +100,41 @@ def cpu_baseline(sample_reps: int) -> dict:
     }
 
 
+def decode_leg(steps: int, warmup: int) -> dict:
+    """Greedy decode of the 28-layer Qwen2.5-7B-shaped random-init model
+    (Q4_K attn q/k/o, gate, up; Q6_K attn v, ffn down, output), fp16 KV cache
+    pre-filled with N(0, 1) to each context, `steps` tokens per context timed
+    wall-clock around one captured-graph decode call (one graph replay per
+    token, token IDs downloaded at the end).  Bytes per token = all weights
+    + the K and V rows read by attention (2 * layers * (ctx+i) * kv_dim * 2 B)."""
+    d = arc.qwen25_7b_dims()
+    log("decode: generating the 7B-shaped model")
+    model = arc.Model(d, seed=SEED)
+    wbytes = model.weight_bytes
+    kvd = d.kv_heads * d.head_dim
+    ctxs = (512, 2048, 4096)
+    sess = arc.Session(model, max(ctxs) + steps)
+    out = {"model": "Qwen2.5-7B shape, 28 layers, Q4_K_M layout, random init",
+           "weight_bytes": wbytes, "steps": steps, "kernels_per_step": None, "contexts": {}}
+    for ctx in ctxs:
+        sess.fill_kv(ctx, SEED + ctx)
+        sess.decode(1234, ctx, max(warmup, 1))  # captures the step graph on first use
+        arc.synchronize()
+        t0 = time.perf_counter()
+        toks, nf = sess.decode(1234, ctx, steps)
+        dt = time.perf_counter() - t0
+        kv_bytes = sum(2 * d.layers * (ctx + i + 1) * kvd * 2 for i in range(steps))
+        gbs = (wbytes * steps + kv_bytes) / dt / 1e9
+        out["contexts"][str(ctx)] = {"tokens_per_s": round(steps / dt, 2), "ms_per_token": round(dt / steps * 1e3, 4),
+                                     "GB/s": round(gbs, 1), "frac_of_peak_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                     "nonfinite": int(nf), "first_tokens": toks[:4].tolist()}
+        log(f"decode ctx {ctx}: {steps / dt:.1f} tok/s, {dt / steps * 1e3:.3f} ms/token, {gbs:.0f} GB/s")
+    out["kernels_per_step"] = sess.kernels_per_step
+    sess.close()
+    model.close()
+    return out
+
+
 def load_traffic() -> dict | None:
     p = os.path.join(ROOT, "profiles", "gateup_swiglu_ffn7b_traffic.json")
     if os.path.exists(p):
@@ -117,6 +152,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--components", action="store_true", help="also time the gate GEMV and LM head")
+    ap.add_argument("--no-decode", action="store_true", help="skip the 28-layer decode leg")
+    ap.add_argument("--decode-steps", type=int, default=64)
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -239,7 +276,7 @@ def main() -> int:
         gate_ms = time_loop(lambda i: arc.gemv(arc.Q4_K, banks[i % B][0], FFN, H, x, s, stream=stream),
                             args.steps, stream)
         comp["q4k_gate_gemv"] = {"us": round(gate_ms * 1e3, 3), "GB/s": round(BYTES_GATE / (gate_ms / 1e3) / 1e9, 1)}
-        del banks
+        banks.clear()
         arc.synchronize()
         lm_h = arc.synth_packed(arc.Q6_K, SEED, 5, VOC, H)
         lm = [arc.DeviceBuffer.from_array(lm_h)]
@@ -257,6 +294,13 @@ def main() -> int:
                                      "GB/s": round(BYTES_LM / (lm_ms / 1e3) / 1e9, 1),
                                      "token": int(out.download(np.uint32)[0])}
         result["components"] = comp
+
+    if not args.no_decode:
+        banks.clear()
+        for buf in (probe_out, x, s, part, y):
+            buf.close()
+        arc.synchronize()
+        result["decode"] = decode_leg(args.decode_steps, 8)
 
     if not args.no_cpu:
         log("cpu baseline")

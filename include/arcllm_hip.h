@@ -158,6 +158,73 @@ int arc_synth_packed(int qtype, uint64_t seed, uint64_t stream, uint32_t rows, u
 int arc_synth_normal(uint64_t seed, uint64_t stream, size_t n, float mean, float sigma,
                      float *out);
 
+/* ------------------------------------------------------- decode runtime */
+/* A Qwen2.5-shaped model (the reference's only model family,
+ * src/arcllm_v1_runtime.cpp:164-211): per layer attn_norm, attn_q/k (Q4_K),
+ * attn_v (Q4_K or Q6_K), q/k/v biases, attn_output (Q4_K), ffn_norm,
+ * ffn_gate/up (Q4_K), ffn_down (Q4_K or Q6_K); token_embd (Q4_K),
+ * output_norm, output (Q6_K).  Norm weights and biases are fp32. */
+#define ARC_MAX_LAYERS 64
+
+typedef struct arc_model_dims {
+    uint32_t hidden, q_heads, kv_heads, head_dim, ffn, vocab, layers;
+    float rms_eps, rope_theta;
+    int32_t v_type[ARC_MAX_LAYERS];    /* ARC_Q4_K or ARC_Q6_K per layer */
+    int32_t down_type[ARC_MAX_LAYERS];
+} arc_model_dims;
+
+/* Tensor slots: global tensors (layer = -1) and per-layer tensors. */
+enum { ARC_T_TOKEN_EMBD = 0, ARC_T_OUTPUT = 1, ARC_T_OUTPUT_NORM = 2, ARC_T_GLOBAL_COUNT = 3 };
+enum {
+    ARC_T_ATTN_NORM = 0, ARC_T_ATTN_Q = 1, ARC_T_ATTN_K = 2, ARC_T_ATTN_V = 3,
+    ARC_T_ATTN_Q_BIAS = 4, ARC_T_ATTN_K_BIAS = 5, ARC_T_ATTN_V_BIAS = 6, ARC_T_ATTN_O = 7,
+    ARC_T_FFN_NORM = 8, ARC_T_FFN_GATE = 9, ARC_T_FFN_UP = 10, ARC_T_FFN_DOWN = 11,
+    ARC_T_LAYER_COUNT = 12
+};
+
+typedef struct arc_model arc_model;
+typedef struct arc_session arc_session;
+
+/* Qwen2.5-7B dims: hidden 3584, 28/4 heads of 128, ffn 18944, vocab 152064,
+ * 28 layers, eps 1e-6, theta 1e6, attn_v and ffn_down Q6_K. */
+int arc_model_dims_qwen25_7b(arc_model_dims *dims);
+/* qtype (ARC_Q4_K, ARC_Q6_K, or 0 for an fp32 vector of K floats), shape
+ * and byte size of one tensor slot (layer -1 for the global tensors). */
+int arc_model_tensor_info(const arc_model_dims *dims, int layer, int which, int *qtype, uint32_t *rows,
+                          uint32_t *K, uint64_t *bytes);
+/* Random-init contents of one tensor slot, host memory: packed tensors as
+ * arc_synth_packed with d_sigma 1e-4, dmin_sigma 7.5e-4 (zero-mean Q4_K rows,
+ * weight std ~0.03), norm weights N(1, 0.05), biases N(0, 0.1);
+ * stream = slot for globals, 100 + 16*layer + slot. */
+int arc_model_synth_tensor(const arc_model_dims *dims, uint64_t seed, int layer, int which, void *out);
+/* Upload a model: tensors[ARC_T_GLOBAL_COUNT + layer*ARC_T_LAYER_COUNT + slot]
+ * (globals first) are host pointers to each slot's bytes (GGUF layout). */
+int arc_model_create(const arc_model_dims *dims, const void *const *tensors, arc_model **out);
+int arc_model_create_synthetic(const arc_model_dims *dims, uint64_t seed, arc_model **out);
+int arc_model_destroy(arc_model *model);
+uint64_t arc_model_weight_bytes(const arc_model *model);
+
+/* A decode session: fp16 KV cache [layer][max_ctx][kv_heads*128] for K and
+ * V (GPU-resident across steps), working buffers and the captured step. */
+int arc_session_create(arc_model *model, uint32_t max_ctx, arc_session **out);
+int arc_session_destroy(arc_session *session);
+/* Device pointers of one layer's K and V cache. */
+int arc_session_kv(arc_session *session, uint32_t layer, void **k, void **v);
+/* Positions [0, ctx) of every layer's K and V := fp16(N(0, 1)), drawn from
+ * (seed, stream 1000000 + 2*layer + {0: K, 1: V}). */
+int arc_session_fill_kv(arc_session *session, uint32_t ctx, uint64_t seed);
+
+#define ARC_DECODE_LOGITS 1   /* keep the last step's logits (arc_session_logits) */
+#define ARC_DECODE_NO_GRAPH 2 /* launch kernels one by one instead of the captured graph */
+/* Greedy decode of n_steps tokens: step i feeds the current token at
+ * position pos + i and writes the argmax (ties to the lowest id) to
+ * out_tokens[i] (host, may be NULL); the next step feeds that token.
+ * *nonfinite = number of non-finite logits seen.  Synchronous. */
+int arc_session_decode(arc_session *session, uint32_t token, uint32_t pos, uint32_t n_steps, int flags,
+                       uint32_t *out_tokens, uint32_t *nonfinite);
+int arc_session_logits(arc_session *session, float *host_logits);
+uint32_t arc_session_kernels_per_step(const arc_session *session);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,6 +9,7 @@
 #include "arc_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
@@ -150,13 +151,55 @@ static float weight_at(int qtype, const uint8_t *blk, uint32_t k)
     return qtype == ORC_Q4_K ? orc_q4k_weight(blk, k) : orc_q6k_weight(blk, k);
 }
 
+/* All 256 weights of one block, each with exactly the operations and operand
+ * order of orc_q4k_weight / orc_q6k_weight (the per-block factors d, dmin,
+ * d*sc and dmin*mn are the same fp32 values those compute per element), so
+ * w[k] == weight_at(qtype, blk, k) bit for bit; it only hoists the repeated
+ * half and scale decodes out of the element loop. */
+static void decode_block(int qtype, const uint8_t *blk, float *w)
+{
+    if (qtype == ORC_Q4_K) {
+        const float d = orc_half_to_float(ld16(blk));
+        const float dmin = orc_half_to_float(ld16(blk + 2));
+        for (uint32_t j = 0; j < 8u; ++j) {
+            uint32_t sc, mn;
+            orc_q4k_scale_min(blk, j, &sc, &mn);
+            const float a = d * (float)sc;
+            const float c = dmin * (float)mn;
+            /* sub-block j holds the low (j even) or high (j odd) nibbles of
+             * bytes 16 + 32*(j/2) .. +31, as orc_q4k_code reads them */
+            const uint8_t *qs = blk + 16u + 32u * (j >> 1);
+            const uint32_t sh = (j & 1u) * 4u;
+            for (uint32_t i = 0; i < 32u; ++i) {
+                const float b = a * (float)((qs[i] >> sh) & 15u);
+                w[32u * j + i] = b - c;
+            }
+        }
+    } else {
+        const float d = orc_half_to_float(ld16(blk + 208));
+        /* the element order of orc_q6k_code: half h, quarter t, lane l */
+        for (uint32_t h = 0; h < 2u; ++h) {
+            const uint8_t *ql = blk + 64u * h, *qh = blk + 128u + 32u * h;
+            const int8_t *sc = (const int8_t *)(blk + 192u + 8u * h);
+            for (uint32_t t = 0; t < 4u; ++t)
+                for (uint32_t l = 0; l < 32u; ++l) {
+                    const uint32_t lo = (ql[l + 32u * (t & 1u)] >> (4u * (t >> 1))) & 15u;
+                    const uint32_t hi = (qh[l] >> (2u * t)) & 3u;
+                    const int q = (int)(lo | (hi << 4)) - 32;
+                    const float a = d * (float)sc[(l >> 4) + 2u * t];
+                    w[128u * h + 32u * t + l] = a * (float)q;
+                }
+        }
+    }
+}
+
 int orc_dequant(int qtype, const uint8_t *w, uint32_t rows, uint32_t K, float *out)
 {
     size_t rb, bb;
     if (row_bytes(qtype, K, &rb, &bb)) return -1;
     for (uint32_t r = 0; r < rows; ++r)
-        for (uint32_t k = 0; k < K; ++k)
-            out[(size_t)r * K + k] = weight_at(qtype, w + r * rb + (k / ORC_QK) * bb, k % ORC_QK);
+        for (uint32_t k = 0; k < K; k += ORC_QK)
+            decode_block(qtype, w + r * rb + (k / ORC_QK) * bb, out + (size_t)r * K + k);
     return 0;
 }
 
@@ -209,9 +252,13 @@ int orc_gemv_r64(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
 #endif
     for (r = 0; r < (long)rows; ++r) {
         const uint8_t *row = w + (size_t)r * rb;
+        float wb[ORC_QK];
         double sum = 0.0;
-        for (uint32_t k = 0; k < K; ++k)
-            sum += (double)weight_at(qtype, row + (k / ORC_QK) * bb, k % ORC_QK) * (double)x[k];
+        for (uint32_t k0 = 0; k0 < K; k0 += ORC_QK) {
+            decode_block(qtype, row + (k0 / ORC_QK) * bb, wb);
+            for (uint32_t k = 0; k < ORC_QK; ++k)
+                sum += (double)wb[k] * (double)x[k0 + k];
+        }
         y[r] = sum + (bias ? (double)bias[r] : 0.0);
     }
     return 0;
@@ -228,9 +275,13 @@ int orc_gemv_r64_xd(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
 #endif
     for (r = 0; r < (long)rows; ++r) {
         const uint8_t *row = w + (size_t)r * rb;
+        float wb[ORC_QK];
         double sum = 0.0;
-        for (uint32_t k = 0; k < K; ++k)
-            sum += (double)weight_at(qtype, row + (k / ORC_QK) * bb, k % ORC_QK) * x[k];
+        for (uint32_t k0 = 0; k0 < K; k0 += ORC_QK) {
+            decode_block(qtype, row + (k0 / ORC_QK) * bb, wb);
+            for (uint32_t k = 0; k < ORC_QK; ++k)
+                sum += (double)wb[k] * x[k0 + k];
+        }
         y[r] = sum;
     }
     return 0;
@@ -252,9 +303,12 @@ int orc_gemv_splitk_r64(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
         for (uint32_t s = 0; s < splits; ++s) {
             double sum = 0.0;
             const uint32_t b0 = s * bps, b1 = (s + 1u) * bps < nb ? (s + 1u) * bps : nb;
-            for (uint32_t b = b0; b < b1; ++b)
+            float wb[ORC_QK];
+            for (uint32_t b = b0; b < b1; ++b) {
+                decode_block(qtype, row + b * bb, wb);
                 for (uint32_t k = 0; k < ORC_QK; ++k)
-                    sum += (double)weight_at(qtype, row + b * bb, k) * (double)x[b * ORC_QK + k];
+                    sum += (double)wb[k] * (double)x[b * ORC_QK + k];
+            }
             part[(size_t)s * rows + (size_t)r] = sum;
         }
     }
@@ -375,7 +429,12 @@ void orc_attention_decode_f64(const double *q, const uint16_t *kc, const uint16_
     const uint32_t hpk = qh / kvh;
     const double scale = 1.0 / sqrt((double)dim);
     const uint32_t T = pos + 1u;
-    for (uint32_t h = 0; h < qh; ++h) {
+    long hh;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (hh = 0; hh < (long)qh; ++hh) {
+        const uint32_t h = (uint32_t)hh;
         const uint32_t kh = h / hpk;
         double mx = -INFINITY, sum = 0.0;
         /* two passes over the keys: max, then exp-sum and weighted values */
@@ -398,4 +457,58 @@ void orc_attention_decode_f64(const double *q, const uint16_t *kc, const uint16_
         }
         for (uint32_t d = 0; d < dim; ++d) out[h * dim + d] /= sum;
     }
+}
+
+/* One decode step, restating the reference's per-token chain
+ * (src/arcllm_v1_runtime.cpp:371-421; CPU helpers
+ * src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1115-1230): embedding row
+ * (Q4_K decode), then per layer attn RMSNorm, q/k/v GEMV + bias, RoPE on
+ * adjacent pairs, K/V stored as fp16 at `pos`, cached GQA over 0..pos,
+ * o GEMV + residual, ffn RMSNorm, SwiGLU(gate, up), down GEMV + residual;
+ * final RMSNorm and the LM head.  Everything after the decoded weights is
+ * fp64; the cache holds fp16(float(value)). */
+int orc_decode_step(const orc_model *m, uint16_t *kc, uint16_t *vc, uint32_t max_ctx, uint32_t pos,
+                    uint32_t token, double *logits)
+{
+    const uint32_t H = m->hidden, KVD = m->kv_heads * m->head_dim, F = m->ffn;
+    if (pos >= max_ctx || token >= m->vocab || m->layers > ORC_MAX_LAYERS) return -1;
+    double *h = malloc(sizeof(double) * H), *xn = malloc(sizeof(double) * H), *q = malloc(sizeof(double) * H);
+    double *kk = malloc(sizeof(double) * KVD), *vv = malloc(sizeof(double) * KVD), *at = malloc(sizeof(double) * H);
+    double *o = malloc(sizeof(double) * H), *g = malloc(sizeof(double) * F), *u = malloc(sizeof(double) * F);
+    double *sw = malloc(sizeof(double) * F);
+    if (!h || !xn || !q || !kk || !vv || !at || !o || !g || !u || !sw) return -2;
+    const size_t erow = (size_t)(H / ORC_QK) * ORC_Q4K_BLOCK_BYTES;
+    for (uint32_t e = 0; e < H; ++e)
+        h[e] = (double)orc_q4k_weight(m->emb + (size_t)token * erow + (e / ORC_QK) * ORC_Q4K_BLOCK_BYTES, e % ORC_QK);
+    for (uint32_t l = 0; l < m->layers; ++l) {
+        uint16_t *kl = kc + (size_t)l * max_ctx * KVD, *vl = vc + (size_t)l * max_ctx * KVD;
+        orc_rmsnorm_f64(h, m->attn_norm[l], H, m->eps, xn);
+        orc_gemv_r64_xd(ORC_Q4_K, m->q[l], H, H, xn, q);
+        orc_gemv_r64_xd(ORC_Q4_K, m->k[l], KVD, H, xn, kk);
+        orc_gemv_r64_xd(m->v_type[l], m->v[l], KVD, H, xn, vv);
+        for (uint32_t i = 0; i < H; ++i) q[i] += (double)m->qb[l][i];
+        for (uint32_t i = 0; i < KVD; ++i) {
+            kk[i] += (double)m->kb[l][i];
+            vv[i] += (double)m->vb[l][i];
+        }
+        orc_rope_f64(q, m->q_heads, m->head_dim, pos, m->theta);
+        orc_rope_f64(kk, m->kv_heads, m->head_dim, pos, m->theta);
+        for (uint32_t i = 0; i < KVD; ++i) {
+            kl[(size_t)pos * KVD + i] = orc_float_to_half_rne((float)kk[i]);
+            vl[(size_t)pos * KVD + i] = orc_float_to_half_rne((float)vv[i]);
+        }
+        orc_attention_decode_f64(q, kl, vl, pos, m->q_heads, m->kv_heads, m->head_dim, at);
+        orc_gemv_r64_xd(ORC_Q4_K, m->o[l], H, H, at, o);
+        for (uint32_t i = 0; i < H; ++i) h[i] += o[i];
+        orc_rmsnorm_f64(h, m->ffn_norm[l], H, m->eps, xn);
+        orc_gemv_r64_xd(ORC_Q4_K, m->gate[l], F, H, xn, g);
+        orc_gemv_r64_xd(ORC_Q4_K, m->up[l], F, H, xn, u);
+        orc_swiglu_f64(g, u, F, sw);
+        orc_gemv_r64_xd(m->down_type[l], m->down[l], H, F, sw, o);
+        for (uint32_t i = 0; i < H; ++i) h[i] += o[i];
+    }
+    orc_rmsnorm_f64(h, m->out_norm, H, m->eps, xn);
+    orc_gemv_r64_xd(ORC_Q6_K, m->out, m->vocab, H, xn, logits);
+    free(h); free(xn); free(q); free(kk); free(vv); free(at); free(o); free(g); free(u); free(sw);
+    return 0;
 }

@@ -77,6 +77,25 @@ void orc_attention_decode_f64(const double *q, const uint16_t *kc, const uint16_
                               double *out);
 uint16_t orc_float_to_half_rne(float f);
 
+/* ---- one greedy decode step of a Qwen2.5-shaped model, fp64 chain ---- */
+#define ORC_MAX_LAYERS 64
+typedef struct {
+    uint32_t hidden, q_heads, kv_heads, head_dim, ffn, vocab, layers;
+    double eps, theta;
+    const uint8_t *emb, *out;
+    const float *out_norm;
+    const float *attn_norm[ORC_MAX_LAYERS], *ffn_norm[ORC_MAX_LAYERS];
+    const uint8_t *q[ORC_MAX_LAYERS], *k[ORC_MAX_LAYERS], *v[ORC_MAX_LAYERS], *o[ORC_MAX_LAYERS];
+    const float *qb[ORC_MAX_LAYERS], *kb[ORC_MAX_LAYERS], *vb[ORC_MAX_LAYERS];
+    const uint8_t *gate[ORC_MAX_LAYERS], *up[ORC_MAX_LAYERS], *down[ORC_MAX_LAYERS];
+    int v_type[ORC_MAX_LAYERS], down_type[ORC_MAX_LAYERS];
+} orc_model;
+/* Feeds `token` at position `pos`: writes this position's K and V (fp16 bits
+ * of the fp32-rounded values) into kc/vc ([layer][max_ctx][kv_heads*head_dim])
+ * and returns the logits.  Returns 0 on success. */
+int orc_decode_step(const orc_model *m, uint16_t *kc, uint16_t *vc, uint32_t max_ctx, uint32_t pos,
+                    uint32_t token, double *logits);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,6 +29,19 @@ class Top2(C.Structure):
                 ("finite", C.c_int)]
 
 
+ORC_MAX_LAYERS = 64
+_PA = _P * ORC_MAX_LAYERS
+
+
+class OrcModel(C.Structure):
+    _fields_ = [("hidden", C.c_uint32), ("q_heads", C.c_uint32), ("kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("ffn", C.c_uint32), ("vocab", C.c_uint32), ("layers", C.c_uint32), ("eps", C.c_double),
+                ("theta", C.c_double), ("emb", _P), ("out", _P), ("out_norm", _P),
+                ("attn_norm", _PA), ("ffn_norm", _PA), ("q", _PA), ("k", _PA), ("v", _PA), ("o", _PA),
+                ("qb", _PA), ("kb", _PA), ("vb", _PA), ("gate", _PA), ("up", _PA), ("down", _PA),
+                ("v_type", C.c_int * ORC_MAX_LAYERS), ("down_type", C.c_int * ORC_MAX_LAYERS)]
+
+
 def oracle() -> C.CDLL:
     global _o
     if _o is None:
@@ -57,6 +70,7 @@ def oracle() -> C.CDLL:
             "orc_rope_f64": ([_P, _U32, _U32, _U32, C.c_double], None),
             "orc_top2": ([_P, _U32, C.POINTER(Top2)], None),
             "orc_attention_decode_f64": ([_P, _P, _P, _U32, _U32, _U32, _U32, _P], None),
+            "orc_decode_step": ([C.POINTER(OrcModel), _P, _P, _U32, _U32, _U32, _P], C.c_int),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -166,3 +180,61 @@ def rel_err(y: np.ndarray, r: np.ndarray) -> float:
     den = np.maximum(np.abs(r), tau)
     den[den == 0] = 1.0
     return float(np.max(np.abs(y - r) / den)) if r.size else 0.0
+
+
+class DecodeOracle:
+    """The fp64 decode-step restatement over host copies of the model tensors
+    (same slot order as arcllm_amd.model_slots) and its own fp16 KV cache."""
+
+    # slot index within a layer -> OrcModel field
+    _LAYER_FIELDS = {0: "attn_norm", 1: "q", 2: "k", 3: "v", 4: "qb", 5: "kb", 6: "vb", 7: "o", 8: "ffn_norm",
+                     9: "gate", 10: "up", 11: "down"}
+
+    def __init__(self, dims, tensors, max_ctx):
+        m = OrcModel()
+        for f in ("hidden", "q_heads", "kv_heads", "head_dim", "ffn", "vocab", "layers"):
+            setattr(m, f, getattr(dims, f))
+        m.eps, m.theta = float(dims.rms_eps), float(dims.rope_theta)
+        m.emb, m.out, m.out_norm = tensors[0].ctypes.data, tensors[1].ctypes.data, tensors[2].ctypes.data
+        for layer in range(dims.layers):
+            for w, field in self._LAYER_FIELDS.items():
+                getattr(m, field)[layer] = tensors[3 + 12 * layer + w].ctypes.data
+            m.v_type[layer] = dims.v_type[layer]
+            m.down_type[layer] = dims.down_type[layer]
+        self.m, self.dims, self.tensors, self.max_ctx = m, dims, tensors, max_ctx
+        kvd = dims.kv_heads * dims.head_dim
+        self.kc = np.zeros(dims.layers * max_ctx * kvd, np.uint16)
+        self.vc = np.zeros_like(self.kc)
+
+    def fill_kv(self, ctx, seed, synth_normal):
+        """Same contents as arc_session_fill_kv: fp16(N(0,1)) per layer and K/V stream."""
+        kvd = self.dims.kv_heads * self.dims.head_dim
+        for layer in range(self.dims.layers):
+            for kv, cache in ((0, self.kc), (1, self.vc)):
+                vals = synth_normal(seed, 1000000 + 2 * layer + kv, ctx * kvd).astype(np.float16).view(np.uint16)
+                base = layer * self.max_ctx * kvd
+                cache[base:base + ctx * kvd] = vals
+
+    def step(self, token, pos):
+        logits = np.empty(self.dims.vocab, np.float64)
+        rc = oracle().orc_decode_step(C.byref(self.m), _p(self.kc), _p(self.vc), self.max_ctx, pos, token,
+                                      _p(logits))
+        assert rc == 0
+        return logits
+
+    def greedy(self, token, pos, n, log=None):
+        """n greedy steps from `token` at `pos`.  Returns (tokens, runner-up
+        tokens, top1-top2 margins, max|logit| per step); `log` gets one line
+        per step."""
+        toks, second, margins, scale = [], [], [], []
+        for i in range(n):
+            lg = self.step(token, pos + i)
+            order = np.argsort(-lg, kind="stable")
+            token = int(order[0])
+            toks.append(token)
+            second.append(int(order[1]))
+            margins.append(float(lg[order[0]] - lg[order[1]]))
+            scale.append(float(np.max(np.abs(lg))))
+            if log is not None:
+                log(f"oracle step {i + 1}/{n} pos={pos + i} token={token} margin={margins[-1]:.4g}")
+        return np.array(toks, np.uint32), np.array(second, np.uint32), np.array(margins), np.array(scale)

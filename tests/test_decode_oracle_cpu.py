@@ -1,0 +1,79 @@
+"""Pins the oracle's decode-step composition (orc_decode_step) against an
+independent numpy fp64 implementation on a tiny model: dequantised weight
+matrices (oracle decode, pinned elsewhere) multiplied with numpy, RoPE as a
+complex rotation of adjacent pairs, softmax attention over the fp16 cache
+with kv head = q head // (q_heads / kv_heads), SwiGLU via scipy expit."""
+import numpy as np
+from scipy.special import expit
+
+import arcllm_amd as arc
+import oracle_lib as orc
+from decode_common import tiny_dims
+
+
+def numpy_step(d, T, kc, vc, max_ctx, pos, token):
+    H, KVD, F = d.hidden, d.kv_heads * 128, d.ffn
+    deq = lambda qt, a, rows, K: orc.dequant(qt, a, rows, K).astype(np.float64)
+
+    def rms(x, w):
+        return x / np.sqrt(np.mean(x * x) + float(d.rms_eps)) * w.astype(np.float64)
+
+    def rope(x, heads):
+        z = x.reshape(heads, 64, 2)
+        c = z[..., 0] + 1j * z[..., 1]
+        c = c * np.exp(1j * pos * float(d.rope_theta) ** (-2.0 * np.arange(64) / 128))
+        return np.stack([c.real, c.imag], -1).reshape(-1)
+
+    h = deq(arc.Q4_K, T[0], d.vocab, H)[token].copy()
+    for layer in range(d.layers):
+        t = lambda w: T[3 + 12 * layer + w]
+        xn = rms(h, t(0))
+        q = deq(arc.Q4_K, t(1), H, H) @ xn + t(4)
+        k = deq(arc.Q4_K, t(2), KVD, H) @ xn + t(5)
+        v = deq(d.v_type[layer], t(3), KVD, H) @ xn + t(6)
+        q, k = rope(q, d.q_heads), rope(k, d.kv_heads)
+        base = layer * max_ctx * KVD
+        kc[base + pos * KVD: base + (pos + 1) * KVD] = k.astype(np.float32).astype(np.float16).view(np.uint16)
+        vc[base + pos * KVD: base + (pos + 1) * KVD] = v.astype(np.float32).astype(np.float16).view(np.uint16)
+        K = kc[base: base + (pos + 1) * KVD].view(np.float16).astype(np.float64).reshape(pos + 1, d.kv_heads, 128)
+        V = vc[base: base + (pos + 1) * KVD].view(np.float16).astype(np.float64).reshape(pos + 1, d.kv_heads, 128)
+        att = np.zeros(H)
+        for hh in range(d.q_heads):
+            g = hh // (d.q_heads // d.kv_heads)
+            s = K[:, g, :] @ q[hh * 128:(hh + 1) * 128] / np.sqrt(128.0)
+            p = np.exp(s - s.max())
+            att[hh * 128:(hh + 1) * 128] = (p / p.sum()) @ V[:, g, :]
+        h = h + deq(arc.Q4_K, t(7), H, H) @ att
+        xn = rms(h, t(8))
+        gg = deq(arc.Q4_K, t(9), F, H) @ xn
+        uu = deq(arc.Q4_K, t(10), F, H) @ xn
+        h = h + deq(d.down_type[layer], t(11), H, F) @ (gg * expit(gg) * uu)
+    return deq(arc.Q6_K, T[1], d.vocab, H) @ rms(h, T[2])
+
+
+def test_oracle_decode_step_matches_numpy_composition():
+    d = tiny_dims(layers=3, vocab=1024)
+    T = arc.synth_model_tensors(d, 0xD0C0DE)
+    max_ctx = 64
+    o = orc.DecodeOracle(d, T, max_ctx)
+    o.fill_kv(20, 77, arc.synth_normal)
+    kc, vc = o.kc.copy(), o.vc.copy()
+    token = 5
+    for pos in (20, 21, 22):
+        lo = o.step(token, pos)
+        ln = numpy_step(d, T, kc, vc, max_ctx, pos, token)
+        np.testing.assert_allclose(lo, ln, rtol=1e-9, atol=1e-9 * np.abs(ln).max())
+        assert np.array_equal(o.kc, kc) and np.array_equal(o.vc, vc)
+        token = int(np.argmax(lo))
+
+
+def test_fill_kv_matches_session_contract():
+    """arc_session_fill_kv draws fp16(N(0,1)) from stream 1000000 + 2*layer + kv;
+    the oracle's fill reproduces it from the same generator."""
+    d = tiny_dims(layers=2, vocab=256)
+    o = orc.DecodeOracle(d, arc.synth_model_tensors(d, 1), 8)
+    o.fill_kv(5, 3, arc.synth_normal)
+    kvd = 256
+    k0 = o.kc[:5 * kvd].view(np.float16).astype(np.float32)
+    assert np.array_equal(k0, arc.synth_normal(3, 1000000, 5 * kvd).astype(np.float16).astype(np.float32))
+    assert np.all(o.kc[5 * kvd: 8 * kvd] == 0)

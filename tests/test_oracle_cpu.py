@@ -270,6 +270,27 @@ def test_r64_matches_float64_matmul(qtype):
 
 
 @pytest.mark.parametrize("qtype", [orc.Q4_K, orc.Q6_K])
+def test_block_dequant_equals_per_element_decode(qtype):
+    """orc_dequant decodes a block at a time; it must equal the per-element
+    definition bit for bit, random bytes and special halves included."""
+    rows, K = 6, 512
+    bb = orc.BLOCK_BYTES[qtype]
+    rng = np.random.default_rng(61)
+    w = rng.integers(0, 256, rows * (K // 256) * bb, dtype=np.uint8)
+    specials = np.array([0x0000, 0x8000, 0x0001, 0x03ff, 0x7bff, 0x7c00, 0xfc00, 0x7e00], np.uint16)
+    off = 0 if qtype == orc.Q4_K else 208
+    blocks = w.reshape(-1, bb)
+    for i in range(len(blocks)):
+        j = i % len(specials)
+        blocks[i, off:off + 2] = specials[j:j + 1].view(np.uint8)
+    deq = orc.dequant(qtype, w, rows, K)
+    fn = O.orc_q4k_weight if qtype == orc.Q4_K else O.orc_q6k_weight
+    per = np.array([[fn(_p(blocks[r * (K // 256) + k // 256]), k % 256) for k in range(K)] for r in range(rows)],
+                   np.float32)
+    assert np.array_equal(deq.view(np.uint32), per.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", [orc.Q4_K, orc.Q6_K])
 def test_r64_one_hot_is_column(qtype):
     rows, K = 16, 512
     w, _ = _synthetic(qtype, rows, K, 6)
