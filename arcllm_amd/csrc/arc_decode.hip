@@ -1,12 +1,13 @@
 // arc_decode.hip -- the single-token greedy decode step of a Qwen2.5-shaped
 // model on gfx950, and its model/session C ABI (include/arcllm_hip.h).
 //
-// One decode step (src/arcllm_v1_runtime.cpp:371-421 restated as 6 launches
+// One decode step (src/arcllm_v1_runtime.cpp:371-421 restated as 7 launches
 // per layer instead of 16 dispatches):
 //   embed      token row of token_embd (Q4_K) -> h                      k_embed_q4k
 //   per layer  [attn RMSNorm + q/k GEMV + bias + RoPE + k -> fp16 cache] k_gemv<Q4,EPI_QKROPE>
 //              [attn RMSNorm + v GEMV + bias -> fp16 cache]              k_gemv<v,EPI_VSTORE>
-//              [cached GQA, chunks of 64 positions, fixed-order merge]   k_attn_decode
+//              [cached GQA over chunks of 64 positions]                  k_attn_chunk
+//              [chunk merge in chunk order]                              k_attn_merge
 //              [o GEMV + residual]                                       k_gemv<Q4,EPI_PLAIN>
 //              [ffn RMSNorm + gate/up GEMV + SwiGLU]                     k_gemv<Q4,EPI_SWIGLU>
 //              [down GEMV + residual]                                    k_gemv<down,EPI_PLAIN>
@@ -28,6 +29,7 @@ namespace arc {
 constexpr int kHeadDim = 128;
 constexpr int kChunk = 64;  // positions per attention workgroup
 constexpr int kMaxHpk = 8;  // q heads per kv head
+constexpr int kMaxChunks = 512;  // contexts up to 32768 positions
 
 // ----------------------------------------------------------------- kernels
 // h = dequant(token_embd[token]) with the bit-exact element formula.
@@ -66,8 +68,8 @@ struct AttnParams {
     const _Float16* kc;       // this layer's K cache [max_ctx][kv_heads*128]
     const _Float16* vc;       // this layer's V cache
     float* out;               // [q_heads*128]
-    float* part;              // [kv_heads][max_chunks][hpk][2 + 128]: m, l, o
-    uint32_t* counters;       // [kv_heads], zero between launches
+    float* po;                // chunk partials o: [kv_heads][max_chunks][hpk][128]
+    float* pml;               // chunk partials (m, l): [kv_heads][max_chunks][hpk][2]
     const DecodeCtl* ctl;
     uint32_t kv_heads, hpk, max_chunks;
     float scale;
@@ -80,59 +82,72 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
-// Cached GQA for one new position (flash-decoding).  Workgroup (c, g) covers
-// positions [64c, 64c+64) of kv head g for its hpk query heads: scores, a
-// chunk-local softmax (max m, sum l) and the weighted V sum o.  The last
-// workgroup of kv head g to finish (atomic ticket) merges the chunks in
-// chunk order: out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).
+// Cached GQA for one new position, flash-decoding stage 1.  Workgroup (c, g)
+// covers positions [64c, 64c+64) of kv head g for its hpk query heads and
+// writes the chunk's softmax max m, sum l and weighted V sum o; every K and V
+// load is issued up front.  Stage 2 (k_attn_merge) combines the chunks; the
+// kernel boundary between the two makes the partials visible without
+// cross-workgroup fences.
 // Semantics: src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1177-1212,
 // shaders/p7_attention_kv_online.comp (kv head = q head / (q_heads/kv_heads)).
-__global__ __launch_bounds__(256) void k_attn_decode(AttnParams a)
+template <int HPK>
+__global__ __launch_bounds__(256) void k_attn_chunk(AttnParams a)
 {
     const uint32_t T = a.ctl->pos + 1;
     const uint32_t nch = (T + kChunk - 1) / kChunk;
     const uint32_t c = blockIdx.x, g = blockIdx.y;
     if (c >= nch) return;
     const uint32_t t0 = c * kChunk, nt = min(uint32_t(kChunk), T - t0);
-    const uint32_t hpk = a.hpk, kvd = a.kv_heads * kHeadDim;
+    constexpr uint32_t hpk = HPK;
+    const uint32_t kvd = a.kv_heads * kHeadDim;
     const int tid = threadIdx.x;
 
-    __shared__ float qs[kMaxHpk][kHeadDim];
-    __shared__ float sc[kMaxHpk][kChunk];
-    __shared__ float ored[4][kMaxHpk][kHeadDim];
-    __shared__ float mh[kMaxHpk], lh[kMaxHpk];
-    __shared__ uint32_t last;
+    __shared__ float qs[HPK][kHeadDim];
+    __shared__ float sc[HPK][kChunk];
+    __shared__ float ored[4][HPK][kHeadDim];
+    __shared__ float mh[HPK], lh[HPK];
 
+    // K: thread -> position tid/4, dims (tid%4)*32 .. +32 (4 x 16 B)
+    const uint32_t tk = uint32_t(tid) >> 2, part = tid & 3;
+    uint4 kraw[4];
+    {
+        const uint4* kp = reinterpret_cast<const uint4*>(a.kc + uint64_t(t0 + min(tk, nt - 1)) * kvd + g * kHeadDim +
+                                                         part * 32);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kraw[i] = kp[i];
+    }
+    // V: thread -> dims 2i, 2i+1 of positions 16*pg .. +16
+    const int vi = tid & 63, pg = tid >> 6;
+    half2_t vraw[16];
+    {
+        const _Float16* vb = a.vc + uint64_t(t0) * kvd + g * kHeadDim + 2 * vi;
+#pragma unroll
+        for (int tt = 0; tt < 16; ++tt)
+            vraw[tt] = *reinterpret_cast<const half2_t*>(vb + uint64_t(min(uint32_t(pg * 16 + tt), nt - 1)) * kvd);
+    }
     for (uint32_t i = tid; i < hpk * kHeadDim; i += 256) qs[i >> 7][i & 127u] = a.q[g * hpk * kHeadDim + i];
     __syncthreads();
-
-    {   // scores: thread -> position tid/4, dims (tid%4)*32 .. +32
-        const uint32_t t = uint32_t(tid) >> 2, part = tid & 3;
-        float s[kMaxHpk];
+    {   // scores
+        float s[HPK];
 #pragma unroll
-        for (int h = 0; h < kMaxHpk; ++h) s[h] = 0.0f;
-        if (t < nt) {
-            const uint4* kp = reinterpret_cast<const uint4*>(a.kc + uint64_t(t0 + t) * kvd + g * kHeadDim + part * 32);
+        for (int h = 0; h < HPK; ++h) s[h] = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint4 raw = kp[i];
-                const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w4[4] = {kraw[i].x, kraw[i].y, kraw[i].z, kraw[i].w};
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float kv = static_cast<float>(__builtin_bit_cast(half2_t, w4[e >> 1])[e & 1]);
-                    const int d = part * 32 + i * 8 + e;
+            for (int e = 0; e < 8; ++e) {
+                const float kv = static_cast<float>(__builtin_bit_cast(half2_t, w4[e >> 1])[e & 1]);
+                const int d = part * 32 + i * 8 + e;
 #pragma unroll
-                    for (int h = 0; h < kMaxHpk; ++h)
-                        if (uint32_t(h) < hpk) s[h] = __builtin_fmaf(qs[h][d], kv, s[h]);
-                }
+                for (int h = 0; h < HPK; ++h) s[h] = __builtin_fmaf(qs[h][d], kv, s[h]);
             }
         }
 #pragma unroll
-        for (int h = 0; h < kMaxHpk; ++h) s[h] = group_sum<4>(s[h]);
-        if (part == 0 && t < nt)
+        for (int h = 0; h < HPK; ++h) s[h] = group_sum<4>(s[h]);
+        if (part == 0 && tk < nt)
 #pragma unroll
-            for (int h = 0; h < kMaxHpk; ++h)
-                if (uint32_t(h) < hpk) sc[h][t] = s[h] * a.scale;
+            for (int h = 0; h < HPK; ++h)
+                sc[h][tk] = s[h] * a.scale;
     }
     __syncthreads();
 
@@ -152,77 +167,142 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnParams a)
     }
     __syncthreads();
 
-    {   // weighted V: thread -> dims 2i, 2i+1 and positions 16*pg .. +16
-        const int i = tid & 63, pg = tid >> 6;
-        float o[kMaxHpk][2];
+    {   // weighted V
+        float o[HPK][2];
 #pragma unroll
-        for (int h = 0; h < kMaxHpk; ++h) o[h][0] = o[h][1] = 0.0f;
+        for (int h = 0; h < HPK; ++h) o[h][0] = o[h][1] = 0.0f;
+#pragma unroll
         for (int tt = 0; tt < 16; ++tt) {
+            // positions past the chunk end carry p = 0 (softmax above) and a
+            // masked V, so the loop needs no branch
             const uint32_t t = pg * 16 + tt;
-            if (t >= nt) break;
-            const half2_t vv =
-                *reinterpret_cast<const half2_t*>(a.vc + uint64_t(t0 + t) * kvd + g * kHeadDim + 2 * i);
-            const float v0 = static_cast<float>(vv.x), v1 = static_cast<float>(vv.y);
+            const bool in = t < nt;
+            const float v0 = in ? static_cast<float>(vraw[tt].x) : 0.0f;
+            const float v1 = in ? static_cast<float>(vraw[tt].y) : 0.0f;
 #pragma unroll
-            for (int h = 0; h < kMaxHpk; ++h) {
-                if (uint32_t(h) < hpk) {
-                    const float p = sc[h][t];
-                    o[h][0] = __builtin_fmaf(p, v0, o[h][0]);
-                    o[h][1] = __builtin_fmaf(p, v1, o[h][1]);
-                }
+            for (int h = 0; h < HPK; ++h) {
+                const float p = sc[h][t];
+                o[h][0] = __builtin_fmaf(p, v0, o[h][0]);
+                o[h][1] = __builtin_fmaf(p, v1, o[h][1]);
             }
         }
 #pragma unroll
-        for (int h = 0; h < kMaxHpk; ++h) {
-            ored[pg][h][2 * i] = o[h][0];
-            ored[pg][h][2 * i + 1] = o[h][1];
+        for (int h = 0; h < HPK; ++h) {
+            ored[pg][h][2 * vi] = o[h][0];
+            ored[pg][h][2 * vi + 1] = o[h][1];
         }
     }
     __syncthreads();
 
-    float* pbase = a.part + (uint64_t(g) * a.max_chunks + c) * hpk * (2 + kHeadDim);
+    const uint32_t phead = uint32_t(g) * a.max_chunks + c;
+    float* po = a.po + uint64_t(phead) * hpk * kHeadDim;
     for (uint32_t idx = tid; idx < hpk * kHeadDim; idx += 256) {
         const uint32_t h = idx >> 7, d = idx & 127u;
-        pbase[h * (2 + kHeadDim) + 2 + d] = ((ored[0][h][d] + ored[1][h][d]) + ored[2][h][d]) + ored[3][h][d];
+        po[idx] = ((ored[0][h][d] + ored[1][h][d]) + ored[2][h][d]) + ored[3][h][d];
     }
     if (uint32_t(tid) < hpk) {
-        pbase[tid * (2 + kHeadDim)] = mh[tid];
-        pbase[tid * (2 + kHeadDim) + 1] = lh[tid];
+        a.pml[(uint64_t(phead) * hpk + tid) * 2] = mh[tid];
+        a.pml[(uint64_t(phead) * hpk + tid) * 2 + 1] = lh[tid];
     }
+}
 
-    // the last workgroup of this kv head merges all chunks, in chunk order
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last = (atomicAdd(&a.counters[g], 1u) == nch - 1) ? 1u : 0u;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
+// hpk is 1..kMaxHpk (checked with the model dims)
+static void launch_attn_chunk(const AttnParams& ap, dim3 grid, hipStream_t st)
+{
+    switch (ap.hpk) {
+    case 1: hipLaunchKernelGGL(k_attn_chunk<1>, grid, dim3(256), 0, st, ap); break;
+    case 2: hipLaunchKernelGGL(k_attn_chunk<2>, grid, dim3(256), 0, st, ap); break;
+    case 3: hipLaunchKernelGGL(k_attn_chunk<3>, grid, dim3(256), 0, st, ap); break;
+    case 4: hipLaunchKernelGGL(k_attn_chunk<4>, grid, dim3(256), 0, st, ap); break;
+    case 5: hipLaunchKernelGGL(k_attn_chunk<5>, grid, dim3(256), 0, st, ap); break;
+    case 6: hipLaunchKernelGGL(k_attn_chunk<6>, grid, dim3(256), 0, st, ap); break;
+    case 7: hipLaunchKernelGGL(k_attn_chunk<7>, grid, dim3(256), 0, st, ap); break;
+    default: hipLaunchKernelGGL(k_attn_chunk<8>, grid, dim3(256), 0, st, ap); break;
+    }
+}
+static_assert(kMaxHpk == 8, "launch_attn_chunk instantiates 1..8");
 
-    __shared__ float Mh[kMaxHpk], Lh[kMaxHpk];
-    const float* gbase = a.part + uint64_t(g) * a.max_chunks * hpk * (2 + kHeadDim);
-    auto ld = [](const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-    if (uint32_t(tid) < hpk) {
-        float M = -INFINITY;
-        for (uint32_t cc = 0; cc < nch; ++cc) M = fmaxf(M, ld(gbase + (cc * hpk + tid) * (2 + kHeadDim)));
-        float L = 0.0f;
-        for (uint32_t cc = 0; cc < nch; ++cc) {
-            const float* pc = gbase + (cc * hpk + tid) * (2 + kHeadDim);
-            L += ld(pc + 1) * expf(ld(pc) - M);
+// Flash-decoding stage 2: workgroup h merges the chunks of query head h in
+// chunk order.  M = max m_c, f_c = e^(m_c - M), L = sum l_c f_c,
+// out = sum o_c f_c / L.  Thread (j, d4) accumulates dims 4*d4 .. +3 over
+// chunks j, j+8, ...; the eight lanes are then summed in order.
+__global__ __launch_bounds__(256) void k_attn_merge(AttnParams a)
+{
+    const uint32_t T = a.ctl->pos + 1;
+    const uint32_t n = (T + kChunk - 1) / kChunk;
+    const uint32_t hq = blockIdx.x, g = hq / a.hpk, hl = hq - g * a.hpk;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    __shared__ float ff[kMaxChunks];
+    __shared__ float wred[2][4];
+    __shared__ float4 ored[8][kHeadDim / 4];
+
+    const float* pml = a.pml + (uint64_t(g) * a.max_chunks * a.hpk + hl) * 2;  // chunk c at + c*hpk*2
+    float mv[kMaxChunks / 256], lv[kMaxChunks / 256];
+    float M = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < kMaxChunks / 256; ++r) {
+        const uint32_t c = uint32_t(r * 256 + tid);
+        mv[r] = -INFINITY;
+        lv[r] = 0.0f;
+        if (c < n) {
+            mv[r] = pml[uint64_t(c) * a.hpk * 2];
+            lv[r] = pml[uint64_t(c) * a.hpk * 2 + 1];
         }
-        Mh[tid] = M;
-        Lh[tid] = L;
+        M = fmaxf(M, mv[r]);
     }
+    M = wave_max(M);
+    if (lane == 0) wred[0][w] = M;
     __syncthreads();
-    for (uint32_t idx = tid; idx < hpk * kHeadDim; idx += 256) {
-        const uint32_t h = idx >> 7, d = idx & 127u;
-        float acc = 0.0f;
-        for (uint32_t cc = 0; cc < nch; ++cc) {
-            const float* pc = gbase + (cc * hpk + h) * (2 + kHeadDim);
-            acc += ld(pc + 2 + d) * expf(ld(pc) - Mh[h]);
+    M = fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3]));
+    float L = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kMaxChunks / 256; ++r) {
+        const uint32_t c = uint32_t(r * 256 + tid);
+        if (c < n) {
+            const float f = expf(mv[r] - M);
+            ff[c] = f;
+            L = __builtin_fmaf(lv[r], f, L);
         }
-        a.out[(g * hpk + h) * kHeadDim + d] = acc / Lh[h];
     }
-    if (tid == 0) a.counters[g] = 0u;
+    L = group_sum<kWave>(L);
+    if (lane == 0) wred[1][w] = L;
+    __syncthreads();
+    L = ((wred[1][0] + wred[1][1]) + wred[1][2]) + wred[1][3];
+
+    const uint32_t j = uint32_t(tid) >> 5, d4 = tid & 31;
+    const float4* src = reinterpret_cast<const float4*>(a.po + (uint64_t(g) * a.max_chunks * a.hpk + hl) * kHeadDim) + d4;
+    const uint32_t stride = a.hpk * (kHeadDim / 4);  // float4s between chunks
+    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t c0 = j; c0 < n; c0 += 64) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = src[uint64_t(min(c0 + 8 * u, n - 1)) * stride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t c = c0 + 8 * u;
+            if (c < n) {
+                const float f = ff[c];
+                acc.x = __builtin_fmaf(v[u].x, f, acc.x);
+                acc.y = __builtin_fmaf(v[u].y, f, acc.y);
+                acc.z = __builtin_fmaf(v[u].z, f, acc.z);
+                acc.w = __builtin_fmaf(v[u].w, f, acc.w);
+            }
+        }
+    }
+    ored[j][d4] = acc;
+    __syncthreads();
+    if (tid < 32) {
+        float4 r = ored[0][tid];
+#pragma unroll
+        for (int k = 1; k < 8; ++k) {
+            r.x += ored[k][tid].x;
+            r.y += ored[k][tid].y;
+            r.z += ored[k][tid].z;
+            r.w += ored[k][tid].w;
+        }
+        const float inv = 1.0f / L;
+        reinterpret_cast<float4*>(a.out + uint64_t(hq) * kHeadDim)[tid] = {r.x * inv, r.y * inv, r.z * inv, r.w * inv};
+    }
 }
 
 // Argmax stage 2 of a decode step: token = argmax, recorded at out[step];
@@ -296,14 +376,15 @@ struct arc_session {
     _Float16* kcache = nullptr;  // [layers][max_ctx][kv_dim]
     _Float16* vcache = nullptr;
     float *h = nullptr, *h1 = nullptr, *q = nullptr, *attn = nullptr, *s = nullptr, *logits = nullptr;
-    float* apart = nullptr;
-    uint32_t* counters = nullptr;
+    float *apo = nullptr, *apml = nullptr;
     double* inv_freq = nullptr;
     arc::ArgBest* best = nullptr;
     uint32_t best_cap = 0;
     arc::DecodeCtl* ctl = nullptr;
     uint32_t* out_tokens = nullptr;
     uint32_t out_cap = 0;
+    arc::DecodeCtl* host_ctl = nullptr;  // pinned staging: [0] upload, [1] download
+    uint32_t* host_tokens = nullptr;     // pinned staging, out_cap entries
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool graph_logits = false;
@@ -315,6 +396,8 @@ struct arc_session {
         if (graph) (void)hipGraphDestroy(graph);
         if (stream) (void)hipStreamDestroy(stream);
         for (void* p : allocations) (void)hipFree(p);
+        if (host_ctl) (void)hipHostFree(host_ctl);
+        if (host_tokens) (void)hipHostFree(host_tokens);
     }
 };
 
@@ -395,15 +478,17 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         ap.kc = kc;
         ap.vc = vc;
         ap.out = S->attn;
-        ap.part = S->apart;
-        ap.counters = S->counters;
+        ap.po = S->apo;
+        ap.pml = S->apml;
         ap.ctl = S->ctl;
         ap.kv_heads = d.kv_heads;
         ap.hpk = d.q_heads / d.kv_heads;
         ap.max_chunks = S->max_chunks;
         ap.scale = 1.0f / std::sqrt(float(kHeadDim));
-        if (!g_dry_run) hipLaunchKernelGGL(k_attn_decode, dim3(S->max_chunks, d.kv_heads), dim3(256), 0, st, ap);
-        if ((rc = chk(hipGetLastError(), "attention"))) return rc;
+        if (!g_dry_run) launch_attn_chunk(ap, dim3(S->max_chunks, d.kv_heads), st);
+        if ((rc = chk(hipGetLastError(), "attention chunks"))) return rc;
+        if (!g_dry_run) hipLaunchKernelGGL(k_attn_merge, dim3(d.q_heads), dim3(256), 0, st, ap);
+        if ((rc = chk(hipGetLastError(), "attention merge"))) return rc;
 
         // o projection + residual: h1 = h + Wo attn
         p = make_params(kFmtQ4, L.o, nullptr, H, H, S->attn);
@@ -620,6 +705,9 @@ uint64_t arc_model_weight_bytes(const arc_model* m) { return m ? m->weight_bytes
 int arc_session_create(arc_model* m, uint32_t max_ctx, arc_session** out)
 {
     if (!m || !out || max_ctx == 0) return set_error(ARC_ERR_INVALID_ARGUMENT, "bad session arguments");
+    if (max_ctx > uint32_t(kMaxChunks * kChunk))
+        return set_error(ARC_ERR_UNSUPPORTED, "max_ctx %u exceeds the supported %d positions", max_ctx,
+                         kMaxChunks * kChunk);
     *out = nullptr;
     std::unique_ptr<arc_session> S(new (std::nothrow) arc_session);
     if (!S) return set_error(ARC_ERR_OUT_OF_MEMORY, "host allocation");
@@ -656,10 +744,11 @@ int arc_session_create(arc_model* m, uint32_t max_ctx, arc_session** out)
     S->s = static_cast<float*>(p);
     if ((rc = alloc(&p, size_t(d.vocab) * fl))) return rc;
     S->logits = static_cast<float*>(p);
-    if ((rc = alloc(&p, size_t(d.kv_heads) * S->max_chunks * (d.q_heads / d.kv_heads) * (2 + kHeadDim) * fl))) return rc;
-    S->apart = static_cast<float*>(p);
-    if ((rc = alloc(&p, d.kv_heads * sizeof(uint32_t)))) return rc;
-    S->counters = static_cast<uint32_t*>(p);
+    const size_t heads_chunks = size_t(d.kv_heads) * S->max_chunks * (d.q_heads / d.kv_heads);
+    if ((rc = alloc(&p, heads_chunks * kHeadDim * fl))) return rc;
+    S->apo = static_cast<float*>(p);
+    if ((rc = alloc(&p, heads_chunks * 2 * fl))) return rc;
+    S->apml = static_cast<float*>(p);
     if ((rc = alloc(&p, 64 * sizeof(double)))) return rc;
     S->inv_freq = static_cast<double*>(p);
     if ((rc = alloc(&p, size_t(S->best_cap) * sizeof(ArgBest)))) return rc;
@@ -668,10 +757,16 @@ int arc_session_create(arc_model* m, uint32_t max_ctx, arc_session** out)
     S->ctl = static_cast<DecodeCtl*>(p);
     if ((rc = alloc(&p, size_t(S->out_cap) * sizeof(uint32_t)))) return rc;
     S->out_tokens = static_cast<uint32_t*>(p);
+    if ((rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&S->host_ctl), 2 * sizeof(DecodeCtl), hipHostMallocDefault),
+                        "pinned ctl")))
+        return rc;
+    if ((rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&S->host_tokens), size_t(S->out_cap) * sizeof(uint32_t),
+                                      hipHostMallocDefault),
+                        "pinned tokens")))
+        return rc;
     double inv[64];
     for (int i = 0; i < 64; ++i) inv[i] = std::pow(double(d.rope_theta), -2.0 * double(i) / double(kHeadDim));
     if ((rc = check_hip(hipMemcpy(S->inv_freq, inv, sizeof(inv), hipMemcpyHostToDevice), "inv_freq"))) return rc;
-    if ((rc = check_hip(hipMemset(S->counters, 0, d.kv_heads * sizeof(uint32_t)), "counters"))) return rc;
     if ((rc = check_hip(hipMemset(S->kcache, 0, kv), "kcache"))) return rc;
     if ((rc = check_hip(hipMemset(S->vcache, 0, kv), "vcache"))) return rc;
     *out = S.release();
@@ -724,8 +819,11 @@ int arc_session_decode(arc_session* s, uint32_t token, uint32_t pos, uint32_t n_
                          s->max_ctx);
     const bool logits = (flags & ARC_DECODE_LOGITS) != 0;
     const bool use_graph = (flags & ARC_DECODE_NO_GRAPH) == 0;
-    DecodeCtl c{pos, token, 0u, 0u};
-    int rc = check_hip(hipMemcpyAsync(s->ctl, &c, sizeof(c), hipMemcpyHostToDevice, s->stream), "ctl upload");
+    // the previous call ended with a stream synchronisation, so the pinned
+    // staging is free to reuse
+    s->host_ctl[0] = DecodeCtl{pos, token, 0u, 0u};
+    int rc = check_hip(hipMemcpyAsync(s->ctl, &s->host_ctl[0], sizeof(DecodeCtl), hipMemcpyHostToDevice, s->stream),
+                       "ctl upload");
     if (rc) return rc;
     if (use_graph && (!s->exec || s->graph_logits != logits)) {
         if (s->exec) {
@@ -766,15 +864,16 @@ int arc_session_decode(arc_session* s, uint32_t token, uint32_t pos, uint32_t n_
             s->kernels_per_step = nk;
         }
     }
-    if (out_tokens && (rc = check_hip(hipMemcpyAsync(out_tokens, s->out_tokens, n_steps * sizeof(uint32_t),
-                                                     hipMemcpyDeviceToHost, s->stream),
-                                      "tokens download")))
+    if ((rc = check_hip(hipMemcpyAsync(s->host_tokens, s->out_tokens, n_steps * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                                       s->stream),
+                        "tokens download")))
         return rc;
-    DecodeCtl after{};
-    if ((rc = check_hip(hipMemcpyAsync(&after, s->ctl, sizeof(after), hipMemcpyDeviceToHost, s->stream), "ctl")))
+    if ((rc = check_hip(hipMemcpyAsync(&s->host_ctl[1], s->ctl, sizeof(DecodeCtl), hipMemcpyDeviceToHost, s->stream),
+                        "ctl download")))
         return rc;
     if ((rc = check_hip(hipStreamSynchronize(s->stream), "decode sync"))) return rc;
-    if (nonfinite) *nonfinite = after.nonfinite;
+    if (out_tokens) std::memcpy(out_tokens, s->host_tokens, n_steps * sizeof(uint32_t));
+    if (nonfinite) *nonfinite = s->host_ctl[1].nonfinite;
     return ARC_OK;
 }
 

@@ -100,7 +100,7 @@ def cpu_baseline(sample_reps: int) -> dict:
     }
 
 
-def decode_leg(steps: int, warmup: int) -> dict:
+def decode_leg(steps: int, warmup: int, graph: bool = True) -> dict:
     """Greedy decode of the 28-layer Qwen2.5-7B-shaped random-init model
     (Q4_K attn q/k/o, gate, up; Q6_K attn v, ffn down, output), fp16 KV cache
     pre-filled with N(0, 1) to each context, `steps` tokens per context timed
@@ -115,13 +115,14 @@ def decode_leg(steps: int, warmup: int) -> dict:
     ctxs = (512, 2048, 4096)
     sess = arc.Session(model, max(ctxs) + steps)
     out = {"model": "Qwen2.5-7B shape, 28 layers, Q4_K_M layout, random init",
+           "launch": "captured graph, one replay per token" if graph else "kernel-by-kernel launches",
            "weight_bytes": wbytes, "steps": steps, "kernels_per_step": None, "contexts": {}}
     for ctx in ctxs:
         sess.fill_kv(ctx, SEED + ctx)
-        sess.decode(1234, ctx, max(warmup, 1))  # captures the step graph on first use
+        sess.decode(1234, ctx, max(warmup, 1), graph=graph)  # captures the step graph on first use
         arc.synchronize()
         t0 = time.perf_counter()
-        toks, nf = sess.decode(1234, ctx, steps)
+        toks, nf = sess.decode(1234, ctx, steps, graph=graph)
         dt = time.perf_counter() - t0
         kv_bytes = sum(2 * d.layers * (ctx + i + 1) * kvd * 2 for i in range(steps))
         gbs = (wbytes * steps + kv_bytes) / dt / 1e9
@@ -154,6 +155,8 @@ def main() -> int:
     ap.add_argument("--components", action="store_true", help="also time the gate GEMV and LM head")
     ap.add_argument("--no-decode", action="store_true", help="skip the 28-layer decode leg")
     ap.add_argument("--decode-steps", type=int, default=64)
+    ap.add_argument("--decode-eager", action="store_true",
+                    help="launch the decode step kernel by kernel instead of replaying its captured graph")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -300,7 +303,7 @@ def main() -> int:
         for buf in (probe_out, x, s, part, y):
             buf.close()
         arc.synchronize()
-        result["decode"] = decode_leg(args.decode_steps, 8)
+        result["decode"] = decode_leg(args.decode_steps, 8, graph=not args.decode_eager)
 
     if not args.no_cpu:
         log("cpu baseline")

@@ -205,7 +205,8 @@ int arc_model_destroy(arc_model *model);
 uint64_t arc_model_weight_bytes(const arc_model *model);
 
 /* A decode session: fp16 KV cache [layer][max_ctx][kv_heads*128] for K and
- * V (GPU-resident across steps), working buffers and the captured step. */
+ * V (GPU-resident across steps), working buffers and the captured step.
+ * max_ctx is 1..32768 (ARC_ERR_UNSUPPORTED above). */
 int arc_session_create(arc_model *model, uint32_t max_ctx, arc_session **out);
 int arc_session_destroy(arc_session *session);
 /* Device pointers of one layer's K and V cache. */
