@@ -37,9 +37,11 @@ __global__ __launch_bounds__(256) void k_embed_q4k(const uint8_t* __restrict__ e
                                                    const DecodeCtl* __restrict__ ctl, float* __restrict__ h)
 {
 #pragma clang fp contract(off)
+    // workgroup b decodes super-block b of the row, one element per thread
     const uint32_t token = ctl->token;
     const uint8_t* row = emb + uint64_t(token) * nb * kQ4Bytes;
-    for (uint32_t e = threadIdx.x; e < nb * kQK; e += 256) {
+    {
+        const uint32_t e = blockIdx.x * kQK + threadIdx.x;
         const uint8_t* b = row + (e >> 8) * kQ4Bytes;
         const uint32_t k = e & 255u, j = k >> 5;
         const float d = f16_bits_to_f32(uint32_t(b[0]) | (uint32_t(b[1]) << 8));
@@ -377,7 +379,7 @@ struct arc_session {
     _Float16* vcache = nullptr;
     float *h = nullptr, *h1 = nullptr, *q = nullptr, *attn = nullptr, *s = nullptr, *logits = nullptr;
     float *apo = nullptr, *apml = nullptr;
-    double* inv_freq = nullptr;
+    float2* rope = nullptr;  // [max_ctx][64] (cos, sin) of pos * theta^(-2p/128)
     arc::ArgBest* best = nullptr;
     uint32_t best_cap = 0;
     arc::DecodeCtl* ctl = nullptr;
@@ -435,7 +437,7 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
     uint32_t n = 0;
     auto chk = [&](hipError_t e, const char* what) { ++n; return check_hip(e, what); };
 
-    if (!g_dry_run) hipLaunchKernelGGL(k_embed_q4k, dim3(1), dim3(256), 0, st, M->emb, H / kQK, S->ctl, S->h);
+    if (!g_dry_run) hipLaunchKernelGGL(k_embed_q4k, dim3(H / kQK), dim3(kQK), 0, st, M->emb, H / kQK, S->ctl, S->h);
     int rc = chk(hipGetLastError(), "embed");
     if (rc) return rc;
 
@@ -454,7 +456,7 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         p.row_split = H;
         p.kv_dim = KVD;
         p.cache = kc;
-        p.inv_freq = S->inv_freq;
+        p.rope = S->rope;
         p.ctl = S->ctl;
         p.y = S->q;
         if ((rc = chk(launch_one<kFmtQ4, EPI_QKROPE, 16, 2>(p, 1, st, nullptr), "q/k projection"))) return rc;
@@ -749,8 +751,8 @@ int arc_session_create(arc_model* m, uint32_t max_ctx, arc_session** out)
     S->apo = static_cast<float*>(p);
     if ((rc = alloc(&p, heads_chunks * 2 * fl))) return rc;
     S->apml = static_cast<float*>(p);
-    if ((rc = alloc(&p, 64 * sizeof(double)))) return rc;
-    S->inv_freq = static_cast<double*>(p);
+    if ((rc = alloc(&p, size_t(max_ctx) * 64 * sizeof(float2)))) return rc;
+    S->rope = static_cast<float2*>(p);
     if ((rc = alloc(&p, size_t(S->best_cap) * sizeof(ArgBest)))) return rc;
     S->best = static_cast<ArgBest*>(p);
     if ((rc = alloc(&p, sizeof(DecodeCtl)))) return rc;
@@ -764,9 +766,18 @@ int arc_session_create(arc_model* m, uint32_t max_ctx, arc_session** out)
                                       hipHostMallocDefault),
                         "pinned tokens")))
         return rc;
-    double inv[64];
-    for (int i = 0; i < 64; ++i) inv[i] = std::pow(double(d.rope_theta), -2.0 * double(i) / double(kHeadDim));
-    if ((rc = check_hip(hipMemcpy(S->inv_freq, inv, sizeof(inv), hipMemcpyHostToDevice), "inv_freq"))) return rc;
+    {   // RoPE factors: angle = pos * theta^(-2p/128) in fp64, cos and sin rounded to fp32
+        double inv[64];
+        for (int i = 0; i < 64; ++i) inv[i] = std::pow(double(d.rope_theta), -2.0 * double(i) / double(kHeadDim));
+        std::vector<float2> tab(size_t(max_ctx) * 64);
+        for (uint32_t t = 0; t < max_ctx; ++t)
+            for (int i = 0; i < 64; ++i) {
+                const double a = double(t) * inv[i];
+                tab[size_t(t) * 64 + i] = make_float2(float(std::cos(a)), float(std::sin(a)));
+            }
+        if ((rc = check_hip(hipMemcpy(S->rope, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice), "rope")))
+            return rc;
+    }
     if ((rc = check_hip(hipMemset(S->kcache, 0, kv), "kcache"))) return rc;
     if ((rc = check_hip(hipMemset(S->vcache, 0, kv), "vcache"))) return rc;
     *out = S.release();

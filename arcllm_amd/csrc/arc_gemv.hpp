@@ -99,7 +99,7 @@ struct GemvParams {
     uint32_t row_split;       // QKROPE: first row taken from w1
     uint32_t kv_dim;          // QKROPE/VSTORE: cache row width (kv heads * 128)
     _Float16* cache;          // QKROPE/VSTORE: this layer's cache, [ctx][kv_dim]
-    const double* inv_freq;   // QKROPE: theta^(-2p/128), p = 0..63
+    const float2* rope;       // QKROPE: (cos, sin) of pos * theta^(-2p/128), [ctx][64]
     const DecodeCtl* ctl;     // QKROPE/VSTORE: current position
 };
 
@@ -340,40 +340,114 @@ __device__ float rms_inv(const float* x, uint32_t n, float eps, float* red)
 // power of two that undoes the unit in which the dot loops read codes as
 // fp16 subnormals (2^-24 for codes in bits 0..5, 2^-20 for Q4_K high
 // nibbles in bits 4..7), which is exact.
+template <int FMT>
+__device__ __forceinline__ void put_group(float* lds, uint32_t gi, const float4 (&q)[4])
+{
+    const uint32_t bl = gi >> 4, v = (gi >> 2) & 3u, t = gi & 3u;
+    float* dst = lds + bl * kXBlk + v * kSlot + t * 16;
+    const float unit = (FMT == kFmtQ4 && (t & 1u)) ? 1048576.0f : 16777216.0f;  // 2^20 : 2^24
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        s += q[i].x;
+        s += q[i].y;
+        s += q[i].z;
+        s += q[i].w;
+        reinterpret_cast<float4*>(dst)[i] = make_float4(q[i].x * unit, q[i].y * unit, q[i].z * unit, q[i].w * unit);
+    }
+    lds[bl * kXBlk + v * kSlot + 64 + t] = s;
+}
+
+template <int FMT>
+__device__ __forceinline__ uint32_t group_elem(uint32_t b0, uint32_t gi)
+{
+    return (b0 + (gi >> 4)) * kQK + x_group_offset<FMT>(int((gi >> 2) & 3u), int(gi & 3u));
+}
+
+__device__ __forceinline__ void ld_group(const float* p, float4 (&q)[4])
+{
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = reinterpret_cast<const float4*>(p)[i];
+}
+
+__device__ __forceinline__ void scale_group(float4 (&q)[4], float inv, const float4 (&w)[4])
+{
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        q[i].x = (q[i].x * inv) * w[i].x;
+        q[i].y = (q[i].y * inv) * w[i].y;
+        q[i].z = (q[i].z * inv) * w[i].z;
+        q[i].w = (q[i].w * inv) * w[i].w;
+    }
+}
+
 template <int FMT, int NT>
 __device__ void stage_x(float* lds, const float* __restrict__ x, uint32_t b0, uint32_t nbl, bool norm,
                         float inv, const float* __restrict__ normw)
 {
     for (uint32_t gi = threadIdx.x; gi < nbl * 16u; gi += NT) {
-        const uint32_t bl = gi >> 4, v = (gi >> 2) & 3u, t = gi & 3u;
-        const uint32_t e = (b0 + bl) * kQK + x_group_offset<FMT>(int(v), int(t));
-        const float4* src = reinterpret_cast<const float4*>(x + e);
+        const uint32_t e = group_elem<FMT>(b0, gi);
         float4 q[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) q[i] = src[i];
+        ld_group(x + e, q);
         if (norm) {
-            const float4* nw = reinterpret_cast<const float4*>(normw + e);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 w = nw[i];
-                q[i].x = (q[i].x * inv) * w.x;
-                q[i].y = (q[i].y * inv) * w.y;
-                q[i].z = (q[i].z * inv) * w.z;
-                q[i].w = (q[i].w * inv) * w.w;
-            }
+            float4 w[4];
+            ld_group(normw + e, w);
+            scale_group(q, inv, w);
         }
-        float* dst = lds + bl * kXBlk + v * kSlot + t * 16;
-        const float unit = (FMT == kFmtQ4 && (t & 1u)) ? 1048576.0f : 16777216.0f;  // 2^20 : 2^24
-        float s = 0.0f;
+        put_group<FMT>(lds, gi, q);
+    }
+}
+
+// RMSNorm fused into the staging of the whole of x (nbl super-blocks): the
+// thread's first group of x and of the norm weights is loaded once, its
+// squares enter the block-wide sum of squares (fp32, fixed order: the
+// thread's other groups first, then the first one, then the wave and
+// workgroup trees), and it is scaled and stored without a second read.
+template <int FMT, int NT>
+__device__ void stage_x_rms(float* lds, const float* __restrict__ x, uint32_t nbl, float eps,
+                            const float* __restrict__ normw, float* red)
+{
+    const uint32_t ng = nbl * 16u, gi0 = threadIdx.x;
+    const bool have = gi0 < ng;
+    float4 q0[4], w0[4];
+    if (have) {
+        const uint32_t e = group_elem<FMT>(0, gi0);
+        ld_group(x + e, q0);
+        ld_group(normw + e, w0);
+    }
+    float ss = 0.0f;
+    for (uint32_t gi = gi0 + NT; gi < ng; gi += NT) {
+        float4 q[4];
+        ld_group(x + group_elem<FMT>(0, gi), q);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            s += q[i].x;
-            s += q[i].y;
-            s += q[i].z;
-            s += q[i].w;
-            reinterpret_cast<float4*>(dst)[i] = make_float4(q[i].x * unit, q[i].y * unit, q[i].z * unit, q[i].w * unit);
+            ss = __builtin_fmaf(q[i].x, q[i].x, ss);
+            ss = __builtin_fmaf(q[i].y, q[i].y, ss);
+            ss = __builtin_fmaf(q[i].z, q[i].z, ss);
+            ss = __builtin_fmaf(q[i].w, q[i].w, ss);
         }
-        lds[bl * kXBlk + v * kSlot + 64 + t] = s;
+    }
+    if (have)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            ss = __builtin_fmaf(q0[i].x, q0[i].x, ss);
+            ss = __builtin_fmaf(q0[i].y, q0[i].y, ss);
+            ss = __builtin_fmaf(q0[i].z, q0[i].z, ss);
+            ss = __builtin_fmaf(q0[i].w, q0[i].w, ss);
+        }
+    ss = block_sum<NT>(ss, red);
+    const float inv = 1.0f / sqrtf(ss / float(nbl * kQK) + eps);
+    if (have) {
+        scale_group(q0, inv, w0);
+        put_group<FMT>(lds, gi0, q0);
+    }
+    for (uint32_t gi = gi0 + NT; gi < ng; gi += NT) {
+        const uint32_t e = group_elem<FMT>(0, gi);
+        float4 q[4], w[4];
+        ld_group(x + e, q);
+        ld_group(normw + e, w);
+        scale_group(q, inv, w);
+        put_group<FMT>(lds, gi, q);
     }
 }
 
@@ -476,9 +550,41 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p)
     Blk bufA[N], bufB[N];
     load(0, 0, bufA);  // weight fetch overlaps the x staging below
 
-    float inv = 1.0f;
-    if (p.flags & F_NORM) inv = rms_inv<kThreads>(p.x, p.nb * kQK, p.eps, red);
-    stage_x<FMT, kThreads>(lds, p.x, kb, nbl, (p.flags & F_NORM) != 0, inv, p.normw);
+    // epilogue operands of the wave's first tile, fetched under the staging
+    float pre_b[RPL], pre_r[RPL];
+    float2 pre_cs = {1.0f, 0.0f};
+    uint32_t pos = 0;
+    {
+        const uint32_t tile0 = min(gw, p.ntiles - 1);
+        if constexpr (EPI == EPI_QKROPE || EPI == EPI_VSTORE) pos = p.ctl->pos;
+#pragma unroll
+        for (int r = 0; r < RPL; ++r) {
+            const uint32_t row = min(tile_row(tile0, r), p.rows - 1);
+            pre_b[r] = 0.0f;
+            pre_r[r] = 0.0f;
+            if constexpr (EPI == EPI_PLAIN) {
+                if (p.flags & F_BIAS) pre_b[r] = p.bias[row];
+                if (p.res) pre_r[r] = p.res[row];
+            } else if constexpr (EPI == EPI_VSTORE) {
+                pre_b[r] = p.bias[row];
+            } else if constexpr (EPI == EPI_QKROPE) {
+                pre_b[r] = row < p.row_split ? p.bias[row] : p.bias2[row - p.row_split];
+            }
+        }
+        if constexpr (EPI == EPI_QKROPE) {
+            const uint32_t row = min(tile_row(tile0, 0), p.rows - 1);
+            const uint32_t lr = row < p.row_split ? row : row - p.row_split;
+            pre_cs = p.rope[uint64_t(pos) * 64 + ((lr & 127u) >> 1)];
+        }
+    }
+
+    if ((p.flags & F_NORM) && kb == 0 && nbl == p.nb) {
+        stage_x_rms<FMT, kThreads>(lds, p.x, nbl, p.eps, p.normw, red);
+    } else {
+        float inv = 1.0f;
+        if (p.flags & F_NORM) inv = rms_inv<kThreads>(p.x, p.nb * kQK, p.eps, red);
+        stage_x<FMT, kThreads>(lds, p.x, kb, nbl, (p.flags & F_NORM) != 0, inv, p.normw);
+    }
     __syncthreads();
 
     float acc[N];
@@ -528,6 +634,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p)
             acc[n] = 0.0f;
         }
         if (v != 0 || bs != 0) return;
+        const bool first = ti == 0;
         if constexpr (EPI == EPI_QKROPE) {
             static_assert(RPL == 2, "RoPE pairs must sit in one lane");
             const uint32_t row = tile_row(tile, 0);  // even; row + 1 is its pair
@@ -535,11 +642,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p)
             const bool isq = row < p.row_split;
             const uint32_t lr = isq ? row : row - p.row_split;
             const float* bias = isq ? p.bias : p.bias2;
-            const float a = tot[0] + bias[lr], b = tot[1] + bias[lr + 1];
-            const uint32_t pos = p.ctl->pos;
-            double sn, cs;
-            sincos(double(pos) * p.inv_freq[(lr & 127u) >> 1], &sn, &cs);
-            const float c = float(cs), sv = float(sn);
+            const float a = tot[0] + (first ? pre_b[0] : bias[lr]), b = tot[1] + (first ? pre_b[1] : bias[lr + 1]);
+            const float2 cs = first ? pre_cs : p.rope[uint64_t(pos) * 64 + ((lr & 127u) >> 1)];
+            const float c = cs.x, sv = cs.y;
             const float ra = a * c - b * sv, rb = a * sv + b * c;
             if (isq) {
                 p.y[lr] = ra;
@@ -558,12 +663,12 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p)
             if constexpr (EPI == EPI_PLAIN) {
                 float val = tot[r];
                 if (p.flags & F_ACCUM) val = p.y[row] + val;
-                if (p.flags & F_BIAS) val = val + p.bias[row];
-                if (p.res) val = p.res[row] + val;
+                if (p.flags & F_BIAS) val = val + (first ? pre_b[r] : p.bias[row]);
+                if (p.res) val = (first ? pre_r[r] : p.res[row]) + val;
                 p.y[row] = val;
             } else if constexpr (EPI == EPI_VSTORE) {
-                const float val = tot[r] + p.bias[row];
-                p.cache[uint64_t(p.ctl->pos) * p.kv_dim + row] = _Float16(val);
+                const float val = tot[r] + (first ? pre_b[r] : p.bias[row]);
+                p.cache[uint64_t(pos) * p.kv_dim + row] = _Float16(val);
             } else if constexpr (EPI == EPI_SWIGLU) {
                 const float g = tot[r], u = tot[RPL + r];
                 p.y[row] = (g / (1.0f + expf(-g))) * u;
@@ -797,6 +902,7 @@ static int run_paneled(int epi, int qtype, GemvParams p, uint32_t splits, hipStr
         q.panel = min(uint32_t(kPanel), p.split_bps - off);
         q.flags = (p.flags & ~(F_ACCUM | F_BIAS)) | (off ? F_ACCUM : 0u) |
                   (off + kPanel >= p.split_bps ? bias_flag : 0u);
+        if (off + kPanel < p.split_bps) q.res = nullptr;  // the residual enters once, with the last panel
         const int rc = check_hip(launch_gemv_epi(epi, qtype, c, q, splits, s, gx), what);
         if (rc) return rc;
     }
