@@ -81,6 +81,7 @@ _SIGS = {
     "arc_synth_packed": [C.c_int, _U64, _U64, _U32, _U32, _F, _F, _P],
     "arc_synth_normal": [_U64, _U64, C.c_size_t, _F, _F, _P],
     "arc_tune_force": [C.c_int, C.c_int],
+    "arc_tune_waves": [C.c_int],
     "arc_probe_read": [_P, C.c_size_t, _P, _U32, _P],
 }
 _RESTYPE = {
@@ -116,6 +117,7 @@ _SIGS.update({
     "arc_session_kv": [_P, _U32, C.POINTER(_P), C.POINTER(_P)],
     "arc_session_fill_kv": [_P, _U32, _U64],
     "arc_session_decode": [_P, _U32, _U32, _U32, C.c_int, _P, C.POINTER(_U32)],
+    "arc_session_prefill": [_P, _P, _U32, _U32, C.c_int, C.POINTER(_U32), C.POINTER(_U32)],
     "arc_session_logits": [_P, _P],
     "arc_session_kernels_per_step": [_P],
 })
@@ -138,6 +140,42 @@ def lib() -> C.CDLL:
             fn.restype = _RESTYPE.get(name, C.c_int)
         _lib = L
     return _lib
+
+
+RUNTIME_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libarcllm_runtime.so")
+CLI_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "arcllm_runtime")
+_rt = None
+
+
+def runtime_lib() -> C.CDLL:
+    """The host runtime library (GGUF reader, generate); raises if not built."""
+    global _rt
+    if _rt is None:
+        if not os.path.exists(RUNTIME_LIB_PATH):
+            raise ArcError(2, f"{RUNTIME_LIB_PATH} not built (run __graft_entry__.build())")
+        L = C.CDLL(RUNTIME_LIB_PATH)
+        L.arcllm_gguf_describe.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t]
+        L.arcllm_gguf_describe.restype = C.c_int
+        _rt = L
+    return _rt
+
+
+def gguf_describe(path: str) -> dict:
+    """JSON description of a GGUF file after the runtime's container checks;
+    raises ArcError with the reader's message when the file is rejected."""
+    import json
+
+    cap = 1 << 20
+    while True:
+        buf = C.create_string_buffer(cap)
+        rc = runtime_lib().arcllm_gguf_describe(path.encode(), buf, cap)
+        if rc == 2:
+            cap *= 4
+            continue
+        text = buf.value.decode(errors="replace")
+        if rc != 0:
+            raise ArcError(1, text)
+        return json.loads(text)
 
 
 def check(rc: int) -> None:
@@ -313,6 +351,11 @@ def tune_force(bs: int, rpl: int) -> None:
     check(lib().arc_tune_force(bs, rpl))
 
 
+def tune_waves(waves: int) -> None:
+    """Force the waves per GEMV workgroup (4 or 8); 0 = automatic."""
+    check(lib().arc_tune_waves(waves))
+
+
 # ------------------------------------------------------- synthetic inputs
 def synth_packed(qtype: int, seed: int, stream: int, rows: int, K: int, d_sigma: float = 0.01,
                  dmin_sigma: float = 0.005) -> np.ndarray:
@@ -415,6 +458,14 @@ class Session:
         flags = (DECODE_LOGITS if logits else 0) | (0 if graph else DECODE_NO_GRAPH)
         check(lib().arc_session_decode(self.handle, token, pos, n_steps, flags, out.ctypes.data, C.byref(nf)))
         return out, nf.value
+
+    def prefill(self, tokens, pos0: int = 0, logits: bool = False, graph: bool = True):
+        """Feed `tokens` at positions pos0.. (teacher-forced); returns (argmax after the last, nonfinite)."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        nxt, nf = C.c_uint32(0), C.c_uint32(0)
+        flags = (DECODE_LOGITS if logits else 0) | (0 if graph else DECODE_NO_GRAPH)
+        check(lib().arc_session_prefill(self.handle, t.ctypes.data, len(t), pos0, flags, C.byref(nxt), C.byref(nf)))
+        return nxt.value, nf.value
 
     def logits(self) -> np.ndarray:
         out = np.empty(self.model.dims.vocab, np.float32)

@@ -1,8 +1,15 @@
-"""Build recipe for the gfx950 HIP library ``arcllm_amd/libarcllm_hip.so``.
+"""Build recipe for the gfx950 HIP library and the host runtime.
 
-Compiles every source under ``arcllm_amd/csrc`` with hipcc for gfx950 and
-links one shared library in-tree.  ``python -m arcllm_amd.build`` or
-``__graft_entry__.build()`` runs it; it always recompiles.
+* ``arcllm_amd/libarcllm_hip.so``: every source under ``arcllm_amd/csrc``
+  compiled with hipcc for gfx950 (the kernels and their C ABI).
+* ``arcllm_amd/libarcllm_runtime.so``: the C++17 host layer under
+  ``arcllm_amd/host`` (GGUF reader, ``arcllm::v1::runtime::generate``),
+  compiled with g++ against the C ABI only.
+* ``arcllm_amd/arcllm_runtime``: the command-line front end.
+
+``python -m arcllm_amd.build`` or ``__graft_entry__.build()`` runs it; it
+always recompiles.  Libraries and the CLI find each other through
+``$ORIGIN`` run paths, so the tree can move as a whole.
 """
 from __future__ import annotations
 
@@ -16,6 +23,11 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libarcllm_hip.so")
+HOST = os.path.join(PKG, "host")
+RUNTIME_LIB = os.path.join(PKG, "libarcllm_runtime.so")
+CLI = os.path.join(PKG, "arcllm_runtime")
+HOST_SOURCES = ["gguf.cpp", "runtime.cpp", "inspect.cpp"]
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep v_pk_{add,mul,fma}_f32 out of the generated code.
@@ -58,8 +70,36 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_host(verbose)
     return LIB
 
 
+def _run(cmd: list[str], what: str) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"{what} failed:\n" + proc.stdout + proc.stderr)
+    if (proc.stdout + proc.stderr).strip():
+        print(proc.stdout + proc.stderr, file=sys.stderr)
+
+
+def build_host(verbose: bool = True) -> None:
+    """g++ build of the host runtime library and CLI over libarcllm_hip.so."""
+    cxx = shutil.which(os.environ.get("CXX", "g++")) or "g++"
+    srcs = [os.path.join(HOST, s) for s in HOST_SOURCES]
+    rpath = "-Wl,-rpath,$ORIGIN"
+    tmp = RUNTIME_LIB + ".tmp"
+    _run([cxx, *HOST_FLAGS, "-shared", "-o", tmp, *srcs, f"-L{PKG}", "-l:libarcllm_hip.so", rpath], "host library")
+    os.replace(tmp, RUNTIME_LIB)
+    tmp = CLI + ".tmp"
+    _run([cxx, *HOST_FLAGS, "-o", tmp, os.path.join(HOST, "cli.cpp"), f"-L{PKG}", "-l:libarcllm_runtime.so",
+          "-l:libarcllm_hip.so", rpath], "CLI")
+    os.replace(tmp, CLI)
+    if verbose:
+        print(f"built {RUNTIME_LIB} and {CLI}")
+
+
 if __name__ == "__main__":
-    build()
+    if sys.argv[1:] == ["host"]:
+        build_host()
+    else:
+        build()

@@ -385,7 +385,7 @@ struct arc_session {
     arc::DecodeCtl* ctl = nullptr;
     uint32_t* out_tokens = nullptr;
     uint32_t out_cap = 0;
-    arc::DecodeCtl* host_ctl = nullptr;  // pinned staging: [0] upload, [1] download
+    arc::DecodeCtl* host_ctl = nullptr;  // pinned staging: [0] download, [1 + i] upload of step i
     uint32_t* host_tokens = nullptr;     // pinned staging, out_cap entries
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -759,7 +759,8 @@ int arc_session_create(arc_model* m, uint32_t max_ctx, arc_session** out)
     S->ctl = static_cast<DecodeCtl*>(p);
     if ((rc = alloc(&p, size_t(S->out_cap) * sizeof(uint32_t)))) return rc;
     S->out_tokens = static_cast<uint32_t*>(p);
-    if ((rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&S->host_ctl), 2 * sizeof(DecodeCtl), hipHostMallocDefault),
+    if ((rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&S->host_ctl), (size_t(max_ctx) + 1) * sizeof(DecodeCtl),
+                                      hipHostMallocDefault),
                         "pinned ctl")))
         return rc;
     if ((rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&S->host_tokens), size_t(S->out_cap) * sizeof(uint32_t),
@@ -819,6 +820,79 @@ int arc_session_fill_kv(arc_session* s, uint32_t ctx, uint64_t seed)
     return ARC_OK;
 }
 
+}  // extern "C"
+
+namespace arc {
+
+// Captures the decode step as a graph on first use (and when the logits
+// flag changes).
+static int ensure_graph(arc_session* s, bool logits)
+{
+    if (s->exec && s->graph_logits == logits) return ARC_OK;
+    if (s->exec) {
+        (void)hipGraphExecDestroy(s->exec);
+        (void)hipGraphDestroy(s->graph);
+        s->exec = nullptr;
+        s->graph = nullptr;
+    }
+    // a dry run fills the launch helpers' occupancy caches (host-side
+    // queries) before the capture starts
+    g_dry_run = true;
+    int rc = launch_step(s, logits, nullptr);
+    g_dry_run = false;
+    if (rc) return rc;
+    if ((rc = check_hip(hipStreamSynchronize(s->stream), "sync"))) return rc;
+    if ((rc = check_hip(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal), "begin capture"))) return rc;
+    uint32_t nk = 0;
+    rc = launch_step(s, logits, &nk);
+    hipGraph_t g = nullptr;
+    const int rc2 = check_hip(hipStreamEndCapture(s->stream, &g), "end capture");
+    if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (rc2) return rc2;
+    s->graph = g;
+    if ((rc = check_hip(hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0), "instantiate"))) return rc;
+    s->graph_logits = logits;
+    s->kernels_per_step = nk;
+    return ARC_OK;
+}
+
+static int run_step(arc_session* s, bool logits, bool use_graph)
+{
+    if (use_graph) return check_hip(hipGraphLaunch(s->exec, s->stream), "graph launch");
+    uint32_t nk = 0;
+    const int rc = launch_step(s, logits, &nk);
+    if (!rc) s->kernels_per_step = nk;
+    return rc;
+}
+
+// Stages step i's control block in pinned memory and queues its upload.  The
+// staging slot stays untouched until the call's final synchronisation.
+static int upload_ctl(arc_session* s, uint32_t i, uint32_t pos, uint32_t token)
+{
+    s->host_ctl[1 + i] = DecodeCtl{pos, token, 0u, 0u};
+    return check_hip(hipMemcpyAsync(s->ctl, &s->host_ctl[1 + i], sizeof(DecodeCtl), hipMemcpyHostToDevice, s->stream),
+                     "ctl upload");
+}
+
+// Downloads the control block after the last step and waits for the stream.
+static int finish_call(arc_session* s, uint32_t* nonfinite, uint32_t* token)
+{
+    int rc = check_hip(hipMemcpyAsync(&s->host_ctl[0], s->ctl, sizeof(DecodeCtl), hipMemcpyDeviceToHost, s->stream),
+                       "ctl download");
+    if (rc) return rc;
+    if ((rc = check_hip(hipStreamSynchronize(s->stream), "decode sync"))) return rc;
+    if (nonfinite) *nonfinite = s->host_ctl[0].nonfinite;
+    if (token) *token = s->host_ctl[0].token;
+    return ARC_OK;
+}
+
+}  // namespace arc
+
+extern "C" {
+
 int arc_session_decode(arc_session* s, uint32_t token, uint32_t pos, uint32_t n_steps, int flags, uint32_t* out_tokens,
                        uint32_t* nonfinite)
 {
@@ -832,60 +906,40 @@ int arc_session_decode(arc_session* s, uint32_t token, uint32_t pos, uint32_t n_
     const bool use_graph = (flags & ARC_DECODE_NO_GRAPH) == 0;
     // the previous call ended with a stream synchronisation, so the pinned
     // staging is free to reuse
-    s->host_ctl[0] = DecodeCtl{pos, token, 0u, 0u};
-    int rc = check_hip(hipMemcpyAsync(s->ctl, &s->host_ctl[0], sizeof(DecodeCtl), hipMemcpyHostToDevice, s->stream),
-                       "ctl upload");
+    int rc = upload_ctl(s, 0, pos, token);
     if (rc) return rc;
-    if (use_graph && (!s->exec || s->graph_logits != logits)) {
-        if (s->exec) {
-            (void)hipGraphExecDestroy(s->exec);
-            (void)hipGraphDestroy(s->graph);
-            s->exec = nullptr;
-            s->graph = nullptr;
-        }
-        // a dry run fills the launch helpers' occupancy caches (host-side
-        // queries) before the capture starts
-        g_dry_run = true;
-        rc = launch_step(s, logits, nullptr);
-        g_dry_run = false;
-        if (rc) return rc;
-        if ((rc = check_hip(hipStreamSynchronize(s->stream), "sync"))) return rc;
-        if ((rc = check_hip(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal), "begin capture")))
-            return rc;
-        uint32_t nk = 0;
-        rc = launch_step(s, logits, &nk);
-        hipGraph_t g = nullptr;
-        const int rc2 = check_hip(hipStreamEndCapture(s->stream, &g), "end capture");
-        if (rc) {
-            if (g) (void)hipGraphDestroy(g);
-            return rc;
-        }
-        if (rc2) return rc2;
-        s->graph = g;
-        if ((rc = check_hip(hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0), "instantiate"))) return rc;
-        s->graph_logits = logits;
-        s->kernels_per_step = nk;
-    }
-    for (uint32_t i = 0; i < n_steps; ++i) {
-        if (use_graph) {
-            if ((rc = check_hip(hipGraphLaunch(s->exec, s->stream), "graph launch"))) return rc;
-        } else {
-            uint32_t nk = 0;
-            if ((rc = launch_step(s, logits, &nk))) return rc;
-            s->kernels_per_step = nk;
-        }
-    }
+    if (use_graph && (rc = ensure_graph(s, logits))) return rc;
+    for (uint32_t i = 0; i < n_steps; ++i)
+        if ((rc = run_step(s, logits, use_graph))) return rc;
     if ((rc = check_hip(hipMemcpyAsync(s->host_tokens, s->out_tokens, n_steps * sizeof(uint32_t), hipMemcpyDeviceToHost,
                                        s->stream),
                         "tokens download")))
         return rc;
-    if ((rc = check_hip(hipMemcpyAsync(&s->host_ctl[1], s->ctl, sizeof(DecodeCtl), hipMemcpyDeviceToHost, s->stream),
-                        "ctl download")))
-        return rc;
-    if ((rc = check_hip(hipStreamSynchronize(s->stream), "decode sync"))) return rc;
+    if ((rc = finish_call(s, nonfinite, nullptr))) return rc;
     if (out_tokens) std::memcpy(out_tokens, s->host_tokens, n_steps * sizeof(uint32_t));
-    if (nonfinite) *nonfinite = s->host_ctl[1].nonfinite;
     return ARC_OK;
+}
+
+int arc_session_prefill(arc_session* s, const uint32_t* tokens, uint32_t n, uint32_t pos0, int flags,
+                        uint32_t* next_token, uint32_t* nonfinite)
+{
+    if (!s || !tokens || n == 0) return set_error(ARC_ERR_INVALID_ARGUMENT, "bad prefill arguments");
+    const arc_model_dims& d = s->model->dims;
+    if (uint64_t(pos0) + n > s->max_ctx)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "positions %u..%u exceed the context %u", pos0, pos0 + n - 1,
+                         s->max_ctx);
+    for (uint32_t i = 0; i < n; ++i)
+        if (tokens[i] >= d.vocab) return set_error(ARC_ERR_INVALID_ARGUMENT, "token %u out of vocabulary", tokens[i]);
+    const bool logits = (flags & ARC_DECODE_LOGITS) != 0;
+    const bool use_graph = (flags & ARC_DECODE_NO_GRAPH) == 0;
+    int rc = 0;
+    if (use_graph && (rc = ensure_graph(s, logits))) return rc;
+    for (uint32_t i = 0; i < n; ++i) {
+        // each step is fed the given token, not the previous step's argmax
+        if ((rc = upload_ctl(s, i, pos0 + i, tokens[i]))) return rc;
+        if ((rc = run_step(s, logits, use_graph))) return rc;
+    }
+    return finish_call(s, nonfinite, next_token);
 }
 
 int arc_session_logits(arc_session* s, float* host_logits)

@@ -38,8 +38,9 @@ int set_error(int code, const char* fmt, ...);
 int check_hip(hipError_t e, const char* what);
 
 constexpr int kPanel = 80;  // max super-block columns of x staged per launch (87 KB LDS)
-constexpr int kWaves = 4;   // waves per GEMV workgroup
+constexpr int kWaves = 4;   // waves per GEMV workgroup (default layout)
 constexpr int kThreads = kWaves * kWave;
+constexpr int kMaxWaves = 8;  // larger workgroups share one staged x when LDS limits residency
 
 // EPI_COLPART: split-K with one super-block column per split -- each quad's
 // own sum is the partial of (column, row), written without a cross-quad
@@ -179,6 +180,24 @@ __device__ __forceinline__ float mix4(uint32_t codes, const float4& x, float acc
     return acc;
 }
 
+// Two mix4 chains advanced in turn (no back-to-back dependent v_fma_mix).
+__device__ __forceinline__ void mix4x2(uint32_t ca, const float4& xa, float& aa, uint32_t cb, const float4& xb,
+                                       float& ab)
+{
+    const uint32_t eva = opaque(ca & 0x00ff00ffu);
+    const uint32_t oda = opaque(__builtin_amdgcn_perm(0u, ca, 0x0c030c01u));
+    const uint32_t evb = opaque(cb & 0x00ff00ffu);
+    const uint32_t odb = opaque(__builtin_amdgcn_perm(0u, cb, 0x0c030c01u));
+    aa = fmix(eva, false, xa.x, aa);
+    ab = fmix(evb, false, xb.x, ab);
+    aa = fmix(oda, false, xa.y, aa);
+    ab = fmix(odb, false, xb.y, ab);
+    aa = fmix(eva, true, xa.z, aa);
+    ab = fmix(evb, true, xb.z, ab);
+    aa = fmix(oda, true, xa.w, aa);
+    ab = fmix(odb, true, xb.w, ab);
+}
+
 __device__ __forceinline__ uint32_t comp(const uint4& q, int i)
 {
     return i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w;
@@ -209,21 +228,23 @@ __device__ __forceinline__ void q4_dot(const Q4Blk (&b)[N], const float* xs, int
             const uint32_t aH = opaque(qa & 0x00f000f0u), aHo = opaque(qa8 & 0x00f000f0u);
             const uint32_t bL = opaque(qb & 0x000f000fu), bLo = opaque(qb8 & 0x000f000fu);
             const uint32_t bH = opaque(qb & 0x00f000f0u), bHo = opaque(qb8 & 0x00f000f0u);
+            // the four group chains advance in turn, so consecutive
+            // v_fma_mix never depend on each other
             a[n][0] = fmix(aL, false, x0.x, a[n][0]);
-            a[n][0] = fmix(aLo, false, x0.y, a[n][0]);
-            a[n][0] = fmix(aL, true, x0.z, a[n][0]);
-            a[n][0] = fmix(aLo, true, x0.w, a[n][0]);
             a[n][1] = fmix(aH, false, x1.x, a[n][1]);
-            a[n][1] = fmix(aHo, false, x1.y, a[n][1]);
-            a[n][1] = fmix(aH, true, x1.z, a[n][1]);
-            a[n][1] = fmix(aHo, true, x1.w, a[n][1]);
             a[n][2] = fmix(bL, false, x2.x, a[n][2]);
-            a[n][2] = fmix(bLo, false, x2.y, a[n][2]);
-            a[n][2] = fmix(bL, true, x2.z, a[n][2]);
-            a[n][2] = fmix(bLo, true, x2.w, a[n][2]);
             a[n][3] = fmix(bH, false, x3.x, a[n][3]);
+            a[n][0] = fmix(aLo, false, x0.y, a[n][0]);
+            a[n][1] = fmix(aHo, false, x1.y, a[n][1]);
+            a[n][2] = fmix(bLo, false, x2.y, a[n][2]);
             a[n][3] = fmix(bHo, false, x3.y, a[n][3]);
+            a[n][0] = fmix(aL, true, x0.z, a[n][0]);
+            a[n][1] = fmix(aH, true, x1.z, a[n][1]);
+            a[n][2] = fmix(bL, true, x2.z, a[n][2]);
             a[n][3] = fmix(bH, true, x3.z, a[n][3]);
+            a[n][0] = fmix(aLo, true, x0.w, a[n][0]);
+            a[n][1] = fmix(aHo, true, x1.w, a[n][1]);
+            a[n][2] = fmix(bLo, true, x2.w, a[n][2]);
             a[n][3] = fmix(bHo, true, x3.w, a[n][3]);
         }
     }
@@ -271,8 +292,7 @@ __device__ __forceinline__ void q6_dot(const Q6Blk (&b)[N], const float* xs, int
                 const uint32_t ql = b[n].ql[h][dw], qh = b[n].qh[h][dw];
                 const uint32_t ua = (ql & 0x0f0f0f0fu) | ((qh << s1) & 0x30303030u);
                 const uint32_t ub = ((ql >> 4) & 0x0f0f0f0fu) | ((qh >> s2) & 0x30303030u);
-                a[n][2 * h] = mix4(ua, xa, a[n][2 * h]);
-                a[n][2 * h + 1] = mix4(ub, xb, a[n][2 * h + 1]);
+                mix4x2(ua, xa, a[n][2 * h], ub, xb, a[n][2 * h + 1]);
             }
         }
     }
@@ -496,11 +516,14 @@ __device__ void wg_argmax(float bv, uint32_t bi, uint32_t nf, ArgBest* out)
 }
 
 // --------------------------------------------------------------- GEMV core
-template <int FMT, int BS, int RPL, int EPI>
-__global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p)
+template <int FMT, int BS, int RPL, int EPI, int W>
+__global__ __launch_bounds__(W * kWave) void k_gemv(GemvParams p)
 {
+    static_assert(W == 4 || W == 8, "4 or 8 waves per workgroup");
+    constexpr int NT = W * kWave;
+    constexpr int PF = 2;  // register buffers in the prefetch ring
     extern __shared__ float lds[];
-    __shared__ float red[kWaves];
+    __shared__ float red[W];
     constexpr int NMAT = (EPI == EPI_SWIGLU) ? 2 : 1;
     constexpr int N = NMAT * RPL;
     constexpr int RG = kWave / (4 * BS);
@@ -519,8 +542,8 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p)
     const uint32_t nbl = min(p.panel, split_end - kb);
     const uint32_t nj = (nbl + BS - 1) / BS;  // block slots per tile, uniform over the wave
 
-    const uint32_t gw = blockIdx.x * kWaves + wave;
-    const uint32_t stride = gridDim.x * kWaves;
+    const uint32_t gw = blockIdx.x * W + wave;
+    const uint32_t stride = gridDim.x * W;
     const uint32_t my_tiles = gw < p.ntiles ? (p.ntiles - gw + stride - 1) / stride : 0u;
     const uint32_t S = my_tiles * nj;
 
@@ -547,8 +570,27 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p)
         }
     };
 
-    Blk bufA[N], bufB[N];
-    load(0, 0, bufA);  // weight fetch overlaps the x staging below
+    // Ring of PF register buffers over the wave's flattened (tile, block
+    // slot) items: PF-1 items are in flight while one is consumed (deeper
+    // rings measured slower: the registers cost more residency than the
+    // extra loads in flight recover).  The
+    // first PF-1 loads are issued before the x staging.  Past the last item
+    // the loads repeat it (a cache hit), keeping the sequence branch-free.
+    Blk buf[PF][N];
+    uint32_t li = 0, lj = 0, lnext = 1;  // next item to load; items issued so far
+    auto advance = [&](uint32_t& i, uint32_t& j) {
+        if (++j == nj) {
+            j = 0;
+            ++i;
+        }
+    };
+    auto load_next = [&](Blk (&b)[N]) {
+        load(li, lj, b);
+        if (lnext < S) advance(li, lj);
+        ++lnext;
+    };
+#pragma unroll
+    for (int u = 0; u < PF - 1; ++u) load_next(buf[u]);
 
     // epilogue operands of the wave's first tile, fetched under the staging
     float pre_b[RPL], pre_r[RPL];
@@ -579,11 +621,11 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p)
     }
 
     if ((p.flags & F_NORM) && kb == 0 && nbl == p.nb) {
-        stage_x_rms<FMT, kThreads>(lds, p.x, nbl, p.eps, p.normw, red);
+        stage_x_rms<FMT, NT>(lds, p.x, nbl, p.eps, p.normw, red);
     } else {
         float inv = 1.0f;
-        if (p.flags & F_NORM) inv = rms_inv<kThreads>(p.x, p.nb * kQK, p.eps, red);
-        stage_x<FMT, kThreads>(lds, p.x, kb, nbl, (p.flags & F_NORM) != 0, inv, p.normw);
+        if (p.flags & F_NORM) inv = rms_inv<NT>(p.x, p.nb * kQK, p.eps, red);
+        stage_x<FMT, NT>(lds, p.x, kb, nbl, (p.flags & F_NORM) != 0, inv, p.normw);
     }
     __syncthreads();
 
@@ -688,39 +730,23 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p)
         }
     };
 
-    // Flattened (tile, block slot) walk with two register buffers: the item
-    // in one buffer is consumed while the next item's loads are in flight.
-    // Past the last item the "next" load repeats the current item (a cache
-    // hit), keeping the load sequence free of branches.
-    uint32_t ti = 0, tj = 0;
-    for (uint32_t s = 0; s < S; s += 2) {
-        uint32_t bi = ti, bj = tj + 1;
-        if (bj == nj) {
-            bj = 0;
-            ++bi;
+    uint32_t ci = 0, cj = 0;  // item being consumed
+    for (uint32_t s = 0; s < S; s += PF) {
+        bool done = false;
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            if (!done) {
+                load_next(buf[(u + PF - 1) % PF]);
+                compute(cj, buf[u]);
+                if constexpr (EPI == EPI_COLPART)
+                    finish_column(ci, cj);
+                else if (cj == nj - 1)
+                    finish(ci);
+                if (s + u + 1 >= S) done = true;
+                advance(ci, cj);
+            }
         }
-        const bool has_b = s + 1 < S;
-        load(has_b ? bi : ti, has_b ? bj : tj, bufB);
-        compute(tj, bufA);
-        if constexpr (EPI == EPI_COLPART)
-            finish_column(ti, tj);
-        else if (tj == nj - 1)
-            finish(ti);
-        if (!has_b) break;
-        uint32_t ci = bi, cj = bj + 1;
-        if (cj == nj) {
-            cj = 0;
-            ++ci;
-        }
-        const bool has_c = s + 2 < S;
-        load(has_c ? ci : bi, has_c ? cj : bj, bufA);
-        compute(bj, bufB);
-        if constexpr (EPI == EPI_COLPART)
-            finish_column(bi, bj);
-        else if (bj == nj - 1)
-            finish(bi);
-        ti = ci;
-        tj = cj;
+        if (done) break;
     }
 
     if constexpr (EPI == EPI_ARGMAX) wg_argmax(best_v, best_i, nonfinite, p.best + blockIdx.x);
@@ -728,7 +754,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvParams p)
 
 // --------------------------------------------------------------- launching
 struct Cfg {
-    int bs, rpl;
+    int bs, rpl, waves;  // quads per row, rows per lane, waves per workgroup (0 = default)
 };
 
 inline int tile_rows(const Cfg& c) { return (kWave / (4 * c.bs)) * c.rpl; }
@@ -749,17 +775,17 @@ static int cu_count()
 }
 
 // Resident workgroups per CU for one kernel instance (cached), >= 1.
-template <int FMT, int EPI, int BS, int RPL>
+template <int FMT, int EPI, int BS, int RPL, int W>
 int occupancy(size_t lds)
 {
     static int occ[kPanel + 1] = {};
     const int slot = int(lds / (kXBlk * sizeof(float)));
     if (!occ[slot]) {
         if (lds > 65536)
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<FMT, BS, RPL, EPI>),
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<FMT, BS, RPL, EPI, W>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
         int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_gemv<FMT, BS, RPL, EPI>, kThreads, lds) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_gemv<FMT, BS, RPL, EPI, W>, W * kWave, lds) != hipSuccess ||
             nb < 1)
             nb = 1;
         occ[slot] = nb;
@@ -770,30 +796,32 @@ int occupancy(size_t lds)
 static thread_local int g_wg_per_cu = 0;  // tuning override of resident workgroups per CU
 static thread_local bool g_dry_run = false;  // size grids and fill caches without launching
 
-template <int FMT, int EPI, int BS, int RPL>
+template <int FMT, int EPI, int BS, int RPL, int W = kWaves>
 hipError_t launch_one(GemvParams p, uint32_t splits, hipStream_t s, uint32_t* grid_x)
 {
-    const Cfg c{BS, RPL};
+    const Cfg c{BS, RPL, W};
     p.ntiles = (p.rows + tile_rows(c) - 1) / tile_rows(c);
     const size_t lds = size_t(p.panel) * kXBlk * sizeof(float);
-    const int per_cu = g_wg_per_cu > 0 ? g_wg_per_cu : occupancy<FMT, EPI, BS, RPL>(lds);
+    const int per_cu = g_wg_per_cu > 0 ? g_wg_per_cu : occupancy<FMT, EPI, BS, RPL, W>(lds);
     const uint64_t resident = uint64_t(per_cu) * cu_count();
-    const uint64_t want = (p.ntiles + kWaves - 1) / kWaves;  // one wave tile per wave
+    const uint64_t want = (p.ntiles + W - 1) / W;  // one wave tile per wave
     uint64_t gx = (resident + splits - 1) / splits;
     if (gx > want) gx = want;  // want <= ceil(rows / 4): one wave tile holds at least one row
     if (gx > 65536) gx = 65536;
     if (gx < 1) gx = 1;
     if (grid_x) *grid_x = uint32_t(gx);
     if (g_dry_run) return hipSuccess;
-    hipLaunchKernelGGL((k_gemv<FMT, BS, RPL, EPI>), dim3(uint32_t(gx), splits), dim3(kThreads), lds, s, p);
+    hipLaunchKernelGGL((k_gemv<FMT, BS, RPL, EPI, W>), dim3(uint32_t(gx), splits), dim3(W * kWave), lds, s, p);
     return hipGetLastError();
 }
 
 template <int FMT, int EPI>
 hipError_t launch_cfg(const Cfg& c, const GemvParams& p, uint32_t splits, hipStream_t s, uint32_t* gx)
 {
-#define ARC_CASE(B, R) \
-    if (c.bs == B && c.rpl == R) return launch_one<FMT, EPI, B, R>(p, splits, s, gx);
+#define ARC_CASE(B, R)                                                         \
+    if (c.bs == B && c.rpl == R)                                               \
+        return c.waves == 8 ? launch_one<FMT, EPI, B, R, 8>(p, splits, s, gx)  \
+                            : launch_one<FMT, EPI, B, R, 4>(p, splits, s, gx);
     ARC_CASE(1, 1) ARC_CASE(1, 2) ARC_CASE(1, 4)
     ARC_CASE(2, 1) ARC_CASE(2, 2) ARC_CASE(2, 4)
     ARC_CASE(4, 1) ARC_CASE(4, 2)
@@ -803,15 +831,26 @@ hipError_t launch_cfg(const Cfg& c, const GemvParams& p, uint32_t splits, hipStr
     return hipErrorInvalidValue;
 }
 
-// Forced configuration for tuning sweeps (bs = 0: automatic).
-static thread_local Cfg g_force{0, 0};
+// Forced configuration for tuning sweeps (bs = 0: automatic; waves = 0: automatic).
+static thread_local Cfg g_force{0, 0, 0};
+static thread_local int g_force_waves = 0;
+
+// Waves per workgroup.  A staged panel wider than 37 super-blocks (> 40 KB
+// of LDS) caps residency at 2-3 workgroups per CU, so 8-wave workgroups
+// share one staged x and double the resident waves (measured +8% on the
+// 74-block FFN-down); the one-column split-K layout also gains from 8.
+inline int choose_waves(int epi, uint32_t /*rows*/, uint32_t blocks)
+{
+    if (g_force_waves) return g_force_waves;
+    return (blocks > 37 || epi == EPI_COLPART) ? 8 : kWaves;
+}
 
 // Automatic lane layout.  Work is balanced over ~2048 resident waves: a
 // layout is preferred when its wave tiles divide evenly over them and its
 // quads are busy (few idle block slots), then when it reuses x over more rows.
 inline Cfg choose_cfg(int epi, uint32_t rows, uint32_t blocks, uint32_t splits)
 {
-    if (g_force.bs) return g_force;
+    if (g_force.bs) return Cfg{g_force.bs, g_force.rpl, choose_waves(epi, rows, blocks)};
     static const Cfg cands[] = {{1, 1}, {1, 2}, {1, 4}, {2, 1}, {2, 2}, {2, 4}, {4, 1}, {4, 2}, {8, 1}, {8, 2}, {16, 1}};
     const double waves = 2048.0;
     Cfg best{1, 1};
@@ -830,6 +869,7 @@ inline Cfg choose_cfg(int epi, uint32_t rows, uint32_t blocks, uint32_t splits)
             best = c;
         }
     }
+    best.waves = choose_waves(epi, rows, blocks);
     return best;
 }
 

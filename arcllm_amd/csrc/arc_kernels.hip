@@ -133,7 +133,7 @@ extern "C" {
 int arc_tune_force(int bs, int rpl)
 {
     if (bs == 0) {
-        g_force = Cfg{0, 0};
+        g_force = Cfg{0, 0, 0};
         g_wg_per_cu = 0;
         return ARC_OK;
     }
@@ -145,10 +145,18 @@ int arc_tune_force(int bs, int rpl)
     static const int ok[][2] = {{1, 1}, {1, 2}, {1, 4}, {2, 1}, {2, 2}, {2, 4}, {4, 1}, {4, 2}, {8, 1}, {8, 2}, {16, 1}};
     for (const auto& c : ok)
         if (c[0] == bs && c[1] == rpl) {
-            g_force = Cfg{bs, rpl};
+            g_force = Cfg{bs, rpl, 0};
             return ARC_OK;
         }
     return set_error(ARC_ERR_INVALID_ARGUMENT, "no kernel instance for bs=%d rpl=%d", bs, rpl);
+}
+
+int arc_tune_waves(int waves)
+{
+    if (waves != 0 && waves != 4 && waves != 8)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "waves per workgroup must be 0 (automatic), 4 or 8");
+    g_force_waves = waves;
+    return ARC_OK;
 }
 
 int arc_dequant(int qtype, const void* w, uint32_t rows, uint32_t K, float* out, arc_stream_t stream)
@@ -219,7 +227,7 @@ int arc_gemv_splitk(int qtype, const void* w, uint32_t rows, uint32_t K, uint32_
         p.split_bps = nb;
         p.panel = nb;
         Cfg c = choose_cfg(EPI_PLAIN, rows, nb, 1);
-        if (c.bs < 8) c = Cfg{8, 1};  // per-slot partials are held in registers: <= 10 slots
+        if (c.bs < 8) c = Cfg{8, 1, c.waves};  // per-slot partials are held in registers: <= 10 slots
         rc = check_hip(launch_gemv_epi(EPI_COLPART, qtype, c, p, 1, s), "split-K pass 1");
     } else {
         rc = run_paneled(EPI_PARTIAL, qtype, p, used, s, "split-K pass 1");

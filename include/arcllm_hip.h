@@ -137,6 +137,9 @@ int arc_lmhead_argmax(int qtype, const void *w, uint32_t rows, uint32_t K, const
  * thread (bs = super-block quads per row: 1,2,4,8,16; rpl = rows per lane:
  * 1,2,4).  bs = 0 restores the automatic choice. */
 int arc_tune_force(int bs, int rpl);
+/* Tuning hook: waves per GEMV workgroup (4 or 8) for later launches on this
+ * host thread; 0 restores the automatic choice. */
+int arc_tune_waves(int waves);
 
 /* Diagnostic: streaming read of `bytes` (16-byte aligned) with `grid`
  * workgroups of 256 lanes, 16 bytes per lane access, xor-folded into
@@ -223,6 +226,14 @@ int arc_session_fill_kv(arc_session *session, uint32_t ctx, uint64_t seed);
  * *nonfinite = number of non-finite logits seen.  Synchronous. */
 int arc_session_decode(arc_session *session, uint32_t token, uint32_t pos, uint32_t n_steps, int flags,
                        uint32_t *out_tokens, uint32_t *nonfinite);
+/* Prompt processing: step i feeds tokens[i] (not the previous argmax) at
+ * position pos0 + i, writing its K and V; *next_token = the argmax after the
+ * last prompt token, *nonfinite = non-finite logits at that last step.  Runs
+ * the decode step per prompt token (src/arcllm_v1_runtime.cpp:340-369 builds
+ * the same prompt pass as one batched graph).  Synchronous. */
+int arc_session_prefill(arc_session *session, const uint32_t *tokens, uint32_t n, uint32_t pos0, int flags,
+                        uint32_t *next_token, uint32_t *nonfinite);
+/* Logits of the last step run with ARC_DECODE_LOGITS (host, vocab floats). */
 int arc_session_logits(arc_session *session, float *host_logits);
 uint32_t arc_session_kernels_per_step(const arc_session *session);
 
