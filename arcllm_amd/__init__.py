@@ -93,7 +93,7 @@ MAX_LAYERS = 64
 T_TOKEN_EMBD, T_OUTPUT, T_OUTPUT_NORM, T_GLOBAL_COUNT = 0, 1, 2, 3
 (T_ATTN_NORM, T_ATTN_Q, T_ATTN_K, T_ATTN_V, T_ATTN_Q_BIAS, T_ATTN_K_BIAS, T_ATTN_V_BIAS, T_ATTN_O,
  T_FFN_NORM, T_FFN_GATE, T_FFN_UP, T_FFN_DOWN, T_LAYER_COUNT) = range(13)
-DECODE_LOGITS, DECODE_NO_GRAPH = 1, 2
+DECODE_LOGITS, DECODE_NO_GRAPH, PREFILL_STEPWISE = 1, 2, 4
 
 
 class ModelDims(C.Structure):
@@ -120,8 +120,10 @@ _SIGS.update({
     "arc_session_prefill": [_P, _P, _U32, _U32, C.c_int, C.POINTER(_U32), C.POINTER(_U32)],
     "arc_session_logits": [_P, _P],
     "arc_session_kernels_per_step": [_P],
+    "arc_session_prefill_kernels": [_P],
 })
-_RESTYPE.update({"arc_model_weight_bytes": _U64, "arc_session_kernels_per_step": _U32})
+_RESTYPE.update({"arc_model_weight_bytes": _U64, "arc_session_kernels_per_step": _U32,
+                 "arc_session_prefill_kernels": _U32})
 
 # Entry points declared in include/*.h that the tests check for.
 EXPORTED = sorted(_SIGS)
@@ -459,11 +461,13 @@ class Session:
         check(lib().arc_session_decode(self.handle, token, pos, n_steps, flags, out.ctypes.data, C.byref(nf)))
         return out, nf.value
 
-    def prefill(self, tokens, pos0: int = 0, logits: bool = False, graph: bool = True):
-        """Feed `tokens` at positions pos0.. (teacher-forced); returns (argmax after the last, nonfinite)."""
+    def prefill(self, tokens, pos0: int = 0, logits: bool = False, graph: bool = True, stepwise: bool = False):
+        """Feed `tokens` at positions pos0..; returns (argmax after the last, nonfinite).  Batched
+        MFMA pass for two or more tokens unless `stepwise` (decode step per token)."""
         t = np.ascontiguousarray(tokens, dtype=np.uint32)
         nxt, nf = C.c_uint32(0), C.c_uint32(0)
-        flags = (DECODE_LOGITS if logits else 0) | (0 if graph else DECODE_NO_GRAPH)
+        flags = (DECODE_LOGITS if logits else 0) | (0 if graph else DECODE_NO_GRAPH) | \
+            (PREFILL_STEPWISE if stepwise else 0)
         check(lib().arc_session_prefill(self.handle, t.ctypes.data, len(t), pos0, flags, C.byref(nxt), C.byref(nf)))
         return nxt.value, nf.value
 
@@ -471,6 +475,10 @@ class Session:
         out = np.empty(self.model.dims.vocab, np.float32)
         check(lib().arc_session_logits(self.handle, out.ctypes.data))
         return out
+
+    @property
+    def prefill_kernels(self) -> int:
+        return int(lib().arc_session_prefill_kernels(self.handle))
 
     @property
     def kernels_per_step(self) -> int:

@@ -16,6 +16,7 @@
 // The position and token live in a device control block, so the step is
 // captured once as a hipGraph and replayed per token.
 #include "arc_gemv.hpp"
+#include "arc_session.hpp"
 
 #include <cmath>
 #include <cstdio>
@@ -25,11 +26,6 @@
 #include <vector>
 
 namespace arc {
-
-constexpr int kHeadDim = 128;
-constexpr int kChunk = 64;  // positions per attention workgroup
-constexpr int kMaxHpk = 8;  // q heads per kv head
-constexpr int kMaxChunks = 512;  // contexts up to 32768 positions
 
 // ----------------------------------------------------------------- kernels
 // h = dequant(token_embd[token]) with the bit-exact element formula.
@@ -77,12 +73,6 @@ struct AttnParams {
     float scale;
 };
 
-__device__ __forceinline__ float wave_max(float v)
-{
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
 
 // Cached GQA for one new position, flash-decoding stage 1.  Workgroup (c, g)
 // covers positions [64c, 64c+64) of kv head g for its hpk query heads and
@@ -345,63 +335,7 @@ __global__ __launch_bounds__(1024) void k_decode_next(const ArgBest* __restrict_
     }
 }
 
-// ------------------------------------------------------------ host objects
-struct Layer {
-    const uint8_t *q, *k, *v, *o, *gate, *up, *down;
-    const float *attn_norm, *ffn_norm, *qb, *kb, *vb;
-    int v_type, down_type;
-};
-
 }  // namespace arc
-
-struct arc_model {
-    arc_model_dims dims{};
-    std::vector<void*> allocations;  // device memory owned by the model
-    const uint8_t* emb = nullptr;
-    const uint8_t* out = nullptr;
-    const float* out_norm = nullptr;
-    std::vector<arc::Layer> layers;
-    uint64_t weight_bytes = 0;
-
-    ~arc_model()
-    {
-        for (void* p : allocations) (void)hipFree(p);
-    }
-};
-
-struct arc_session {
-    arc_model* model = nullptr;
-    uint32_t max_ctx = 0;
-    uint32_t max_chunks = 0;
-    hipStream_t stream = nullptr;
-    std::vector<void*> allocations;
-    _Float16* kcache = nullptr;  // [layers][max_ctx][kv_dim]
-    _Float16* vcache = nullptr;
-    float *h = nullptr, *h1 = nullptr, *q = nullptr, *attn = nullptr, *s = nullptr, *logits = nullptr;
-    float *apo = nullptr, *apml = nullptr;
-    float2* rope = nullptr;  // [max_ctx][64] (cos, sin) of pos * theta^(-2p/128)
-    arc::ArgBest* best = nullptr;
-    uint32_t best_cap = 0;
-    arc::DecodeCtl* ctl = nullptr;
-    uint32_t* out_tokens = nullptr;
-    uint32_t out_cap = 0;
-    arc::DecodeCtl* host_ctl = nullptr;  // pinned staging: [0] download, [1 + i] upload of step i
-    uint32_t* host_tokens = nullptr;     // pinned staging, out_cap entries
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
-    bool graph_logits = false;
-    uint32_t kernels_per_step = 0;
-
-    ~arc_session()
-    {
-        if (exec) (void)hipGraphExecDestroy(exec);
-        if (graph) (void)hipGraphDestroy(graph);
-        if (stream) (void)hipStreamDestroy(stream);
-        for (void* p : allocations) (void)hipFree(p);
-        if (host_ctl) (void)hipHostFree(host_ctl);
-        if (host_tokens) (void)hipHostFree(host_tokens);
-    }
-};
 
 namespace arc {
 
@@ -428,6 +362,27 @@ static int dims_ok(const arc_model_dims& d)
 
 // Launch one decode step on the session stream (captured into a graph by the
 // caller, or run eagerly).  Returns the number of kernels launched.
+int launch_lm_head(arc_session* S, const float* x, bool logits, hipStream_t st)
+{
+    const arc_model* M = S->model;
+    const arc_model_dims& d = M->dims;
+    const uint32_t H = d.hidden;
+    GemvParams p = make_params(kFmtQ6, M->out, nullptr, d.vocab, H, x);
+    p.flags = F_NORM;
+    p.normw = M->out_norm;
+    p.eps = d.rms_eps;
+    p.y = logits ? S->logits : nullptr;
+    p.best = S->best;
+    uint32_t gx = 0;
+    int rc = check_hip(launch_gemv_epi(EPI_ARGMAX, kFmtQ6, choose_cfg(EPI_ARGMAX, d.vocab, H / kQK, 1), p, 1, st, &gx),
+                       "lm head");
+    if (rc) return rc;
+    if (gx > S->best_cap) return set_error(ARC_ERR_UNSUPPORTED, "internal: argmax grid %u > %u", gx, S->best_cap);
+    if (!g_dry_run)
+        hipLaunchKernelGGL(k_decode_next, dim3(1), dim3(1024), 0, st, S->best, gx, S->ctl, S->out_tokens, S->out_cap);
+    return check_hip(hipGetLastError(), "argmax");
+}
+
 static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
 {
     arc_model* M = S->model;
@@ -518,20 +473,8 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
     }
 
     // output RMSNorm + LM head + argmax
-    GemvParams p = make_params(kFmtQ6, M->out, nullptr, d.vocab, H, S->h);
-    p.flags = F_NORM;
-    p.normw = M->out_norm;
-    p.eps = d.rms_eps;
-    p.y = logits ? S->logits : nullptr;
-    p.best = S->best;
-    uint32_t gx = 0;
-    if ((rc = chk(launch_gemv_epi(EPI_ARGMAX, kFmtQ6, choose_cfg(EPI_ARGMAX, d.vocab, H / kQK, 1), p, 1, st, &gx),
-                  "lm head")))
-        return rc;
-    if (gx > S->best_cap) return set_error(ARC_ERR_UNSUPPORTED, "internal: argmax grid %u > %u", gx, S->best_cap);
-    if (!g_dry_run)
-        hipLaunchKernelGGL(k_decode_next, dim3(1), dim3(1024), 0, st, S->best, gx, S->ctl, S->out_tokens, S->out_cap);
-    if ((rc = chk(hipGetLastError(), "argmax"))) return rc;
+    if ((rc = launch_lm_head(S, S->h, logits, st))) return rc;
+    n += 2;
     if (nkernels) *nkernels = n;
     return ARC_OK;
 }
@@ -933,11 +876,18 @@ int arc_session_prefill(arc_session* s, const uint32_t* tokens, uint32_t n, uint
     const bool logits = (flags & ARC_DECODE_LOGITS) != 0;
     const bool use_graph = (flags & ARC_DECODE_NO_GRAPH) == 0;
     int rc = 0;
+    if (n > 1 && (flags & ARC_PREFILL_STEPWISE) == 0) {
+        // batched MFMA prompt pass
+        if ((rc = run_prefill(s, tokens, n, pos0, logits))) return rc;
+        return finish_call(s, nonfinite, next_token);
+    }
     if (use_graph && (rc = ensure_graph(s, logits))) return rc;
+    s->prefill_kernels = 0;
     for (uint32_t i = 0; i < n; ++i) {
         // each step is fed the given token, not the previous step's argmax
         if ((rc = upload_ctl(s, i, pos0 + i, tokens[i]))) return rc;
         if ((rc = run_step(s, logits, use_graph))) return rc;
+        s->prefill_kernels += s->kernels_per_step;
     }
     return finish_call(s, nonfinite, next_token);
 }
@@ -950,5 +900,7 @@ int arc_session_logits(arc_session* s, float* host_logits)
 }
 
 uint32_t arc_session_kernels_per_step(const arc_session* s) { return s ? s->kernels_per_step : 0; }
+
+uint32_t arc_session_prefill_kernels(const arc_session* s) { return s ? s->prefill_kernels : 0; }
 
 }  // extern "C"

@@ -15,6 +15,25 @@ constexpr int kQ6Bytes = 210;    // Q6_K super-block
 constexpr int kFmtQ4 = 12;
 constexpr int kFmtQ6 = 14;
 
+// Defined in arc_runtime.cpp.
+int set_error(int code, const char* fmt, ...);
+int check_hip(hipError_t e, const char* what);
+
+// Decode-step control block in device memory: the graph of one decode step
+// reads the position and token from here, and the argmax writes them back.
+struct DecodeCtl {
+    uint32_t pos;        // position of the token being decoded
+    uint32_t token;      // its id
+    uint32_t step;       // tokens generated so far in this run
+    uint32_t nonfinite;  // non-finite logits seen so far
+};
+struct ArgBest {
+    float val;
+    uint32_t idx;
+    uint32_t nonfinite;
+    uint32_t pad;
+};
+
 // --------------------------------------------------------------- x staging
 // Each super-block column of x is held in LDS as 4 lane slots of 68 floats:
 // the 64 x values one lane of a 4-lane "quad" multiplies against (four
@@ -104,6 +123,29 @@ __device__ __forceinline__ float group_sum(float v)
     if constexpr (N >= 16) v += dpp_f<0x140>(v);  // row_mirror: other 8 of 16
     if constexpr (N >= 32) v += __shfl_xor(v, 16);
     if constexpr (N >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+// Sum over a workgroup of NT threads (fixed order: wave trees, then the
+// waves in order); every thread receives the total.
+template <int NT>
+__device__ inline float block_sum(float v, float* red)
+{
+    v = group_sum<kWave>(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NT / kWave; ++i) s += red[i];
+    return s;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) v = fmaxf(v, __shfl_xor(v, off));
     return v;
 }
 

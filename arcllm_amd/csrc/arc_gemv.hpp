@@ -33,9 +33,6 @@
 
 namespace arc {
 
-// Defined in arc_runtime.cpp.
-int set_error(int code, const char* fmt, ...);
-int check_hip(hipError_t e, const char* what);
 
 constexpr int kPanel = 80;  // max super-block columns of x staged per launch (87 KB LDS)
 constexpr int kWaves = 4;   // waves per GEMV workgroup (default layout)
@@ -59,22 +56,7 @@ enum Epi {
     EPI_VSTORE = 6
 };
 
-// Decode-step control block in device memory: the graph of one decode step
-// reads the position and token from here, and the argmax writes them back.
-struct DecodeCtl {
-    uint32_t pos;        // position of the token being decoded
-    uint32_t token;      // its id
-    uint32_t step;       // tokens generated so far in this run
-    uint32_t nonfinite;  // non-finite logits seen so far
-};
 enum Flag : uint32_t { F_NORM = 1u, F_ACCUM = 2u, F_BIAS = 4u };
-
-struct ArgBest {
-    float val;
-    uint32_t idx;
-    uint32_t nonfinite;
-    uint32_t pad;
-};
 
 struct GemvParams {
     const uint8_t* w0;
@@ -329,20 +311,6 @@ __device__ __forceinline__ void blk_load(const uint8_t* blk, int v, typename Blk
 }
 
 // ------------------------------------------------------------- reductions
-template <int NT>
-__device__ float block_sum(float v, float* red)
-{
-    v = group_sum<kWave>(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NT / kWave; ++i) s += red[i];
-    return s;
-}
-
 // 1/sqrt(mean(x^2) + eps) over n elements, fp32, fixed reduction order.
 template <int NT>
 __device__ float rms_inv(const float* x, uint32_t n, float eps, float* red)

@@ -167,9 +167,10 @@ RunResult generate(const RunRequest& request)
           "prefill");
     if (nonfinite) fail("non-finite prefill logits");
     result.generated_token_ids.push_back(next);
-    const uint32_t per_step = arc_session_kernels_per_step(session.get());
-    result.stats.prefill_dispatches = uint32_t(seq) * per_step;
-    result.stats.prefill_submits = uint32_t(seq);
+    // the prompt pass: kernel launches as issued; submits = passes of up to
+    // 256 prompt rows (one decode-step graph launch per token for a 1-token prompt)
+    result.stats.prefill_dispatches = arc_session_prefill_kernels(session.get());
+    result.stats.prefill_submits = seq > 1 ? uint32_t((seq + 255) / 256) : 1u;
     result.stats.finite = true;
 
     const uint32_t steps = request.max_new_tokens - 1;

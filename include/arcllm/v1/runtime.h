@@ -14,8 +14,9 @@
  *    sidecar_path, evidence_profile and request_within_validated_domain are
  *    accepted and not used by generation, as in the reference.
  *
- * RuntimeStats: "dispatches" are kernel launches and "submits" are
- * captured-graph launches; route_a_steps counts decode steps run on the
+ * RuntimeStats: "dispatches" are kernel launches; decode "submits" are
+ * captured-graph launches (one per step) and prefill "submits" are batched
+ * prompt passes of up to 256 rows; route_a_steps counts decode steps run on the
  * direct packed kernels (route B, the EXEC148 repack, is not used), so
  * acquire/evict and the b_* / p* counters stay 0.
  */

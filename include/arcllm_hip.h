@@ -226,16 +226,22 @@ int arc_session_fill_kv(arc_session *session, uint32_t ctx, uint64_t seed);
  * *nonfinite = number of non-finite logits seen.  Synchronous. */
 int arc_session_decode(arc_session *session, uint32_t token, uint32_t pos, uint32_t n_steps, int flags,
                        uint32_t *out_tokens, uint32_t *nonfinite);
-/* Prompt processing: step i feeds tokens[i] (not the previous argmax) at
- * position pos0 + i, writing its K and V; *next_token = the argmax after the
- * last prompt token, *nonfinite = non-finite logits at that last step.  Runs
- * the decode step per prompt token (src/arcllm_v1_runtime.cpp:340-369 builds
- * the same prompt pass as one batched graph).  Synchronous. */
+/* Prompt processing: tokens[i] at position pos0 + i for i < n, writing every
+ * position's K and V; *next_token = the argmax after the last prompt token,
+ * *nonfinite = non-finite logits at that last position.  n >= 2 runs the
+ * batched prompt pass (src/arcllm_v1_runtime.cpp:340-369): MFMA GEMMs over
+ * all prompt rows (fp16 operands: X and the dequantised weights, fp32
+ * accumulation), causal GQA, the LM head on the last row only; passes of 256
+ * rows.  n = 1 or ARC_PREFILL_STEPWISE replays the decode step per token
+ * with teacher forcing instead.  Synchronous. */
+#define ARC_PREFILL_STEPWISE 4
 int arc_session_prefill(arc_session *session, const uint32_t *tokens, uint32_t n, uint32_t pos0, int flags,
                         uint32_t *next_token, uint32_t *nonfinite);
 /* Logits of the last step run with ARC_DECODE_LOGITS (host, vocab floats). */
 int arc_session_logits(arc_session *session, float *host_logits);
 uint32_t arc_session_kernels_per_step(const arc_session *session);
+/* Kernel launches of the last arc_session_prefill call. */
+uint32_t arc_session_prefill_kernels(const arc_session *session);
 
 #ifdef __cplusplus
 }

@@ -287,6 +287,36 @@ int orc_gemv_r64_xd(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
     return 0;
 }
 
+/* R64 with both operands rounded to binary16 first (RNE from fp32: the
+ * decoded weight, and the input element rounded to fp32): the arithmetic of
+ * an fp16-operand matrix unit with exact products and fp64 accumulation. */
+int orc_gemv_r64_f16(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
+                     const double *x, double *y)
+{
+    size_t rb, bb;
+    if (row_bytes(qtype, K, &rb, &bb)) return -1;
+    float *x16 = malloc(sizeof(float) * K);
+    if (!x16) return -2;
+    for (uint32_t k = 0; k < K; ++k) x16[k] = orc_half_to_float(orc_float_to_half_rne((float)x[k]));
+    long r;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (r = 0; r < (long)rows; ++r) {
+        const uint8_t *row = w + (size_t)r * rb;
+        float wb[ORC_QK];
+        double sum = 0.0;
+        for (uint32_t k0 = 0; k0 < K; k0 += ORC_QK) {
+            decode_block(qtype, row + (k0 / ORC_QK) * bb, wb);
+            for (uint32_t k = 0; k < ORC_QK; ++k)
+                sum += (double)orc_half_to_float(orc_float_to_half_rne(wb[k])) * (double)x16[k0 + k];
+        }
+        y[r] = sum;
+    }
+    free(x16);
+    return 0;
+}
+
 int orc_gemv_splitk_r64(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
                         uint32_t splits, const float *x, double *part)
 {
@@ -470,6 +500,16 @@ void orc_attention_decode_f64(const double *q, const uint16_t *kc, const uint16_
 int orc_decode_step(const orc_model *m, uint16_t *kc, uint16_t *vc, uint32_t max_ctx, uint32_t pos,
                     uint32_t token, double *logits)
 {
+    return orc_decode_step_ex(m, kc, vc, max_ctx, pos, token, 0, logits);
+}
+
+typedef int (*orc_layer_gemv)(int, const uint8_t *, uint32_t, uint32_t, const double *, double *);
+
+int orc_decode_step_ex(const orc_model *m, uint16_t *kc, uint16_t *vc, uint32_t max_ctx, uint32_t pos,
+                       uint32_t token, int f16_operands, double *logits)
+{
+    /* the layer GEMVs (not the LM head) optionally with fp16 operands */
+    const orc_layer_gemv lg = f16_operands ? orc_gemv_r64_f16 : orc_gemv_r64_xd;
     const uint32_t H = m->hidden, KVD = m->kv_heads * m->head_dim, F = m->ffn;
     if (pos >= max_ctx || token >= m->vocab || m->layers > ORC_MAX_LAYERS) return -1;
     double *h = malloc(sizeof(double) * H), *xn = malloc(sizeof(double) * H), *q = malloc(sizeof(double) * H);
@@ -483,9 +523,9 @@ int orc_decode_step(const orc_model *m, uint16_t *kc, uint16_t *vc, uint32_t max
     for (uint32_t l = 0; l < m->layers; ++l) {
         uint16_t *kl = kc + (size_t)l * max_ctx * KVD, *vl = vc + (size_t)l * max_ctx * KVD;
         orc_rmsnorm_f64(h, m->attn_norm[l], H, m->eps, xn);
-        orc_gemv_r64_xd(ORC_Q4_K, m->q[l], H, H, xn, q);
-        orc_gemv_r64_xd(ORC_Q4_K, m->k[l], KVD, H, xn, kk);
-        orc_gemv_r64_xd(m->v_type[l], m->v[l], KVD, H, xn, vv);
+        lg(ORC_Q4_K, m->q[l], H, H, xn, q);
+        lg(ORC_Q4_K, m->k[l], KVD, H, xn, kk);
+        lg(m->v_type[l], m->v[l], KVD, H, xn, vv);
         for (uint32_t i = 0; i < H; ++i) q[i] += (double)m->qb[l][i];
         for (uint32_t i = 0; i < KVD; ++i) {
             kk[i] += (double)m->kb[l][i];
@@ -498,13 +538,13 @@ int orc_decode_step(const orc_model *m, uint16_t *kc, uint16_t *vc, uint32_t max
             vl[(size_t)pos * KVD + i] = orc_float_to_half_rne((float)vv[i]);
         }
         orc_attention_decode_f64(q, kl, vl, pos, m->q_heads, m->kv_heads, m->head_dim, at);
-        orc_gemv_r64_xd(ORC_Q4_K, m->o[l], H, H, at, o);
+        lg(ORC_Q4_K, m->o[l], H, H, at, o);
         for (uint32_t i = 0; i < H; ++i) h[i] += o[i];
         orc_rmsnorm_f64(h, m->ffn_norm[l], H, m->eps, xn);
-        orc_gemv_r64_xd(ORC_Q4_K, m->gate[l], F, H, xn, g);
-        orc_gemv_r64_xd(ORC_Q4_K, m->up[l], F, H, xn, u);
+        lg(ORC_Q4_K, m->gate[l], F, H, xn, g);
+        lg(ORC_Q4_K, m->up[l], F, H, xn, u);
         orc_swiglu_f64(g, u, F, sw);
-        orc_gemv_r64_xd(m->down_type[l], m->down[l], H, F, sw, o);
+        lg(m->down_type[l], m->down[l], H, F, sw, o);
         for (uint32_t i = 0; i < H; ++i) h[i] += o[i];
     }
     orc_rmsnorm_f64(h, m->out_norm, H, m->eps, xn);

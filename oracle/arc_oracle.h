@@ -46,6 +46,10 @@ int orc_gemv_r64(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
 /* R64 with an fp64 input vector (for inputs produced by the fp64 chain). */
 int orc_gemv_r64_xd(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
                     const double *x, double *y);
+/* R64 with fp16 operands: each decoded weight and each input element
+ * (rounded to fp32) rounded to binary16 (RNE), exact products, fp64 sum. */
+int orc_gemv_r64_f16(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
+                     const double *x, double *y);
 /* Split-K partials in fp64: part[s*rows + r] = sum over blocks
  * [s*bps, min((s+1)*bps, nb)) of row r. */
 int orc_gemv_splitk_r64(int qtype, const uint8_t *w, uint32_t rows, uint32_t K,
@@ -95,6 +99,11 @@ typedef struct {
  * and returns the logits.  Returns 0 on success. */
 int orc_decode_step(const orc_model *m, uint16_t *kc, uint16_t *vc, uint32_t max_ctx, uint32_t pos,
                     uint32_t token, double *logits);
+/* The same with f16_operands != 0: every layer GEMV (q, k, v, o, gate, up,
+ * down; not the LM head) uses orc_gemv_r64_f16 -- the arithmetic of the
+ * batched MFMA prompt pass. */
+int orc_decode_step_ex(const orc_model *m, uint16_t *kc, uint16_t *vc, uint32_t max_ctx, uint32_t pos,
+                       uint32_t token, int f16_operands, double *logits);
 
 #ifdef __cplusplus
 }

@@ -62,6 +62,7 @@ def oracle() -> C.CDLL:
             "orc_gemv_r64": ([C.c_int, _P, _U32, _U32, _P, _P, _P], C.c_int),
             "orc_gemv_splitk_r64": ([C.c_int, _P, _U32, _U32, _U32, _P, _P], C.c_int),
             "orc_gemv_r64_xd": ([C.c_int, _P, _U32, _U32, _P, _P], C.c_int),
+            "orc_gemv_r64_f16": ([C.c_int, _P, _U32, _U32, _P, _P], C.c_int),
             "orc_rmsnorm_f32": ([_P, _P, _U32, C.c_float, _P], None),
             "orc_rmsnorm_f64": ([_P, _P, _U32, C.c_double, _P], None),
             "orc_swiglu_f32": ([_P, _P, _U32, _P], None),
@@ -71,6 +72,7 @@ def oracle() -> C.CDLL:
             "orc_top2": ([_P, _U32, C.POINTER(Top2)], None),
             "orc_attention_decode_f64": ([_P, _P, _P, _U32, _U32, _U32, _U32, _P], None),
             "orc_decode_step": ([C.POINTER(OrcModel), _P, _P, _U32, _U32, _U32, _P], C.c_int),
+            "orc_decode_step_ex": ([C.POINTER(OrcModel), _P, _P, _U32, _U32, _U32, C.c_int, _P], C.c_int),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -126,6 +128,13 @@ def gemv_r64_xd(qtype: int, w: np.ndarray, rows: int, K: int, x: np.ndarray) -> 
     x = np.ascontiguousarray(x, dtype=np.float64)
     y = np.empty(rows, dtype=np.float64)
     assert oracle().orc_gemv_r64_xd(qtype, _p(w), rows, K, _p(x), _p(y)) == 0
+    return y
+
+
+def gemv_r64_f16(qtype: int, w: np.ndarray, rows: int, K: int, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    y = np.empty(rows, dtype=np.float64)
+    assert oracle().orc_gemv_r64_f16(qtype, _p(w), rows, K, _p(x), _p(y)) == 0
     return y
 
 
@@ -190,7 +199,7 @@ class DecodeOracle:
     _LAYER_FIELDS = {0: "attn_norm", 1: "q", 2: "k", 3: "v", 4: "qb", 5: "kb", 6: "vb", 7: "o", 8: "ffn_norm",
                      9: "gate", 10: "up", 11: "down"}
 
-    def __init__(self, dims, tensors, max_ctx):
+    def __init__(self, dims, tensors, max_ctx, f16_operands=False):
         m = OrcModel()
         for f in ("hidden", "q_heads", "kv_heads", "head_dim", "ffn", "vocab", "layers"):
             setattr(m, f, getattr(dims, f))
@@ -202,6 +211,7 @@ class DecodeOracle:
             m.v_type[layer] = dims.v_type[layer]
             m.down_type[layer] = dims.down_type[layer]
         self.m, self.dims, self.tensors, self.max_ctx = m, dims, tensors, max_ctx
+        self.f16 = 1 if f16_operands else 0
         kvd = dims.kv_heads * dims.head_dim
         self.kc = np.zeros(dims.layers * max_ctx * kvd, np.uint16)
         self.vc = np.zeros_like(self.kc)
@@ -217,8 +227,8 @@ class DecodeOracle:
 
     def step(self, token, pos):
         logits = np.empty(self.dims.vocab, np.float64)
-        rc = oracle().orc_decode_step(C.byref(self.m), _p(self.kc), _p(self.vc), self.max_ctx, pos, token,
-                                      _p(logits))
+        rc = oracle().orc_decode_step_ex(C.byref(self.m), _p(self.kc), _p(self.vc), self.max_ctx, pos, token,
+                                         self.f16, _p(logits))
         assert rc == 0
         return logits
 

@@ -2,8 +2,11 @@
 independent numpy fp64 implementation on a tiny model: dequantised weight
 matrices (oracle decode, pinned elsewhere) multiplied with numpy, RoPE as a
 complex rotation of adjacent pairs, softmax attention over the fp16 cache
-with kv head = q head // (q_heads / kv_heads), SwiGLU via scipy expit."""
+with kv head = q head // (q_heads / kv_heads), SwiGLU via scipy expit.  The
+fp16-operand mode (the batched prompt pass's arithmetic) is pinned the same
+way, with numpy's own binary16 rounding of the layer-GEMM operands."""
 import numpy as np
+import pytest
 from scipy.special import expit
 
 import arcllm_amd as arc
@@ -11,9 +14,14 @@ import oracle_lib as orc
 from decode_common import tiny_dims
 
 
-def numpy_step(d, T, kc, vc, max_ctx, pos, token):
+def numpy_step(d, T, kc, vc, max_ctx, pos, token, f16=False):
     H, KVD, F = d.hidden, d.kv_heads * 128, d.ffn
-    deq = lambda qt, a, rows, K: orc.dequant(qt, a, rows, K).astype(np.float64)
+    deq_exact = lambda qt, a, rows, K: orc.dequant(qt, a, rows, K).astype(np.float64)
+    if f16:  # layer GEMMs: both operands rounded to binary16 (weights from fp32, inputs via fp32)
+        deq = lambda qt, a, rows, K: orc.dequant(qt, a, rows, K).astype(np.float16).astype(np.float64)
+        op = lambda x: x.astype(np.float32).astype(np.float16).astype(np.float64)
+    else:
+        deq, op = deq_exact, (lambda x: x)
 
     def rms(x, w):
         return x / np.sqrt(np.mean(x * x) + float(d.rms_eps)) * w.astype(np.float64)
@@ -24,10 +32,10 @@ def numpy_step(d, T, kc, vc, max_ctx, pos, token):
         c = c * np.exp(1j * pos * float(d.rope_theta) ** (-2.0 * np.arange(64) / 128))
         return np.stack([c.real, c.imag], -1).reshape(-1)
 
-    h = deq(arc.Q4_K, T[0], d.vocab, H)[token].copy()
+    h = deq_exact(arc.Q4_K, T[0], d.vocab, H)[token].copy()
     for layer in range(d.layers):
         t = lambda w: T[3 + 12 * layer + w]
-        xn = rms(h, t(0))
+        xn = op(rms(h, t(0)))
         q = deq(arc.Q4_K, t(1), H, H) @ xn + t(4)
         k = deq(arc.Q4_K, t(2), KVD, H) @ xn + t(5)
         v = deq(d.v_type[layer], t(3), KVD, H) @ xn + t(6)
@@ -43,25 +51,26 @@ def numpy_step(d, T, kc, vc, max_ctx, pos, token):
             s = K[:, g, :] @ q[hh * 128:(hh + 1) * 128] / np.sqrt(128.0)
             p = np.exp(s - s.max())
             att[hh * 128:(hh + 1) * 128] = (p / p.sum()) @ V[:, g, :]
-        h = h + deq(arc.Q4_K, t(7), H, H) @ att
-        xn = rms(h, t(8))
+        h = h + deq(arc.Q4_K, t(7), H, H) @ op(att)
+        xn = op(rms(h, t(8)))
         gg = deq(arc.Q4_K, t(9), F, H) @ xn
         uu = deq(arc.Q4_K, t(10), F, H) @ xn
-        h = h + deq(d.down_type[layer], t(11), H, F) @ (gg * expit(gg) * uu)
-    return deq(arc.Q6_K, T[1], d.vocab, H) @ rms(h, T[2])
+        h = h + deq(d.down_type[layer], t(11), H, F) @ op(gg * expit(gg) * uu)
+    return deq_exact(arc.Q6_K, T[1], d.vocab, H) @ rms(h, T[2])
 
 
-def test_oracle_decode_step_matches_numpy_composition():
+@pytest.mark.parametrize("f16", [False, True])
+def test_oracle_decode_step_matches_numpy_composition(f16):
     d = tiny_dims(layers=3, vocab=1024)
     T = arc.synth_model_tensors(d, 0xD0C0DE)
     max_ctx = 64
-    o = orc.DecodeOracle(d, T, max_ctx)
+    o = orc.DecodeOracle(d, T, max_ctx, f16_operands=f16)
     o.fill_kv(20, 77, arc.synth_normal)
     kc, vc = o.kc.copy(), o.vc.copy()
     token = 5
     for pos in (20, 21, 22):
         lo = o.step(token, pos)
-        ln = numpy_step(d, T, kc, vc, max_ctx, pos, token)
+        ln = numpy_step(d, T, kc, vc, max_ctx, pos, token, f16)
         np.testing.assert_allclose(lo, ln, rtol=1e-9, atol=1e-9 * np.abs(ln).max())
         assert np.array_equal(o.kc, kc) and np.array_equal(o.vc, vc)
         token = int(np.argmax(lo))
@@ -77,3 +86,17 @@ def test_fill_kv_matches_session_contract():
     k0 = o.kc[:5 * kvd].view(np.float16).astype(np.float32)
     assert np.array_equal(k0, arc.synth_normal(3, 1000000, 5 * kvd).astype(np.float16).astype(np.float32))
     assert np.all(o.kc[5 * kvd: 8 * kvd] == 0)
+
+
+def test_f16_gemv_is_exact_products_of_rounded_operands():
+    rng = np.random.default_rng(4)
+    for qt in (arc.Q4_K, arc.Q6_K):
+        rows, K = 24, 768
+        w = arc.synth_packed(qt, 9, 3, rows, K)
+        x = rng.standard_normal(K) * 3.0
+        got = orc.gemv_r64_f16(qt, w, rows, K, x)
+        ref = orc.dequant(qt, w, rows, K).astype(np.float16).astype(np.float64) @ \
+            x.astype(np.float32).astype(np.float16).astype(np.float64)
+        np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12 * np.abs(ref).max())
+        # and it differs from the exact-operand product (the rounding is real)
+        assert not np.array_equal(got, orc.gemv_r64_xd(qt, w, rows, K, x))

@@ -29,9 +29,12 @@ def _log(msg):
 
 
 def oracle_generate(d, T, prompt, max_new):
-    o = orc.DecodeOracle(d, T, len(prompt) + max_new)
+    # prompts of two or more tokens take the batched pass (fp16 GEMM operands):
+    # the oracle follows it with its fp16-operand mode, then decodes exactly
+    o = orc.DecodeOracle(d, T, len(prompt) + max_new, f16_operands=len(prompt) > 1)
     for i, t in enumerate(prompt):
         lg = o.step(int(t), i)
+    o.f16 = 0
     order = np.argsort(-lg, kind="stable")
     first, second0 = int(order[0]), int(order[1])
     m0, s0 = float(lg[order[0]] - lg[order[1]]), float(np.max(np.abs(lg)))
@@ -75,7 +78,8 @@ def test_generate_cli_matches_oracle(tmp_path):
     assert tokens_match(gpu, ref, second, margins, scale) >= max_new // 2
     st = res["stats"]
     per_step = 3 + 7 * d.layers
-    assert st["prefill_dispatches"] == len(prompt) * per_step and st["prefill_submits"] == len(prompt)
+    # batched prompt pass: embed, 12 launches per layer, LM head + next token
+    assert st["prefill_dispatches"] == 1 + 12 * d.layers + 2 and st["prefill_submits"] == 1
     assert st["decode_dispatches_per_step"] == per_step and st["decode_submits_per_step"] == 1
     assert st["decode_steps"] == max_new - 1 and st["route_a_steps"] == max_new - 1
     assert st["route_b_steps"] == 0 and st["finite"] is True
@@ -104,11 +108,11 @@ def test_session_prefill_logits_and_continuation():
     s = arc.Session(model, 64)
     nxt, nf = s.prefill(prompt, logits=True)
     lg = s.logits()
-    o = orc.DecodeOracle(d, T, 64)
+    o = orc.DecodeOracle(d, T, 64, f16_operands=True)
     for i, t in enumerate(prompt):
         ref = o.step(int(t), i)
     assert nf == 0
-    assert orc.rel_err(lg, ref) <= 1e-3
+    assert np.max(np.abs(lg - ref)) <= 5e-3 * np.max(np.abs(ref))  # normwise, as tests/test_prefill_gpu.py
     assert nxt == int(np.argmax(lg))
     # prefill in two calls (positions continue) gives the same next token, and
     # eager launches agree with the captured graph
