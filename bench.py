@@ -35,6 +35,7 @@ H, FFN, VOC = 3584, 18944, 152064
 SPLITS = 74
 SEED = 0x0B5E_7C4_2026
 PEAK_HBM_GBS = 8000.0
+PEAK_FP16_FLOPS = 2.5e15  # dense fp16 MFMA, MI355X
 
 Q4_ROW = (H // 256) * 144
 Q6_ROW_DOWN = (FFN // 256) * 210
@@ -132,7 +133,40 @@ def decode_leg(steps: int, warmup: int, graph: bool = True) -> dict:
         log(f"decode ctx {ctx}: {steps / dt:.1f} tok/s, {dt / steps * 1e3:.3f} ms/token, {gbs:.0f} GB/s")
     out["kernels_per_step"] = sess.kernels_per_step
     sess.close()
+    out["prefill"] = prefill_leg(model, d)
     model.close()
+    return out
+
+
+def prefill_leg(model, d, reps: int = 5) -> dict:
+    """The 256-token prompt pass (config 4): TTFT = wall-clock of one
+    arc_session_prefill call on a fresh session (token upload, 28 layers of
+    MFMA GEMMs + causal GQA, LM head + argmax on the last row, control-block
+    download), median of `reps` after a warmup.  MFMA work = the projections,
+    2 * 256 * sum(N*K) over the layers."""
+    S = 256
+    prompt = (np.arange(S, dtype=np.uint64) * 7919 + 13) % d.vocab
+    prompt = prompt.astype(np.uint32)
+    kvd = d.kv_heads * d.head_dim
+    nk = 0
+    for layer in range(d.layers):
+        nk += (d.hidden + 2 * kvd) * d.hidden + d.hidden * d.hidden + 2 * d.ffn * d.hidden + d.hidden * d.ffn
+    flops = 2.0 * S * nk
+    sess = arc.Session(model, S + 64)
+    sess.prefill(prompt)  # warmup: buffers, code objects
+    times = []
+    for _ in range(reps):
+        arc.synchronize()
+        t0 = time.perf_counter()
+        tok, nf = sess.prefill(prompt)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[reps // 2]
+    log(f"prefill 256: TTFT {t * 1e3:.2f} ms, {flops / t / 1e12:.1f} TFLOP/s on the MFMA projections")
+    out = {"tokens": S, "ttft_ms": round(t * 1e3, 3), "mfma_flops": flops,
+           "mfma_tflops": round(flops / t / 1e12, 2), "mfma_frac_of_dense_fp16_peak": round(flops / t / PEAK_FP16_FLOPS, 4),
+           "kernels": sess.prefill_kernels, "next_token": int(tok), "nonfinite": int(nf),
+           "note": "fp16 GEMM operands (activations, dequantised weights), fp32 accumulation"}
+    sess.close()
     return out
 
 
