@@ -82,35 +82,87 @@ struct PfGemm {
     uint32_t lds_out;
 };
 
-// 8 bytes from a 2-byte-aligned address inside a Q6_K block, from dword
-// loads at the dword-aligned floor, realigned in registers.  All dwords read
-// lie inside the 210-byte block for the offsets used below.
-__device__ __forceinline__ void ld8_2a(const uint8_t* p, uint32_t& lo, uint32_t& hi)
-{
-    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p)) & 3u;
-    const uint32_t* a = reinterpret_cast<const uint32_t*>(p - sh);
-    const uint32_t d0 = a[0], d1 = a[1];
-    const uint32_t d2 = sh ? a[2] : 0u;
-    lo = __builtin_amdgcn_alignbyte(d1, d0, sh);
-    hi = __builtin_amdgcn_alignbyte(d2, d1, sh);
-}
+// K order inside a super-block.  The GEMM sums over K, so X and W only have
+// to agree on which element each MFMA K slot holds.  Step t (0..7) of half
+// block hb gives the lane of half kh (lane / 32) the 8 consecutive elements
+// hb*128 + acol(t) + kh*16 .. +7, with acol(t) = (t/2)*32 + (t%2)*8, so one
+// lane's elements for a whole super-block come from a few contiguous 16-byte
+// pieces of the packed block:
+//   Q4_K: qs bytes c*32 + kh*16 .. +15 of chunk c hold elements
+//         c*64 + kh*16 + 0..15 (low nibbles) and c*64 + 32 + kh*16 + 0..15
+//         (high nibbles); steps t = 4(c%2) + r take the low nibbles of bytes
+//         0..7 (r=0) / 8..15 (r=1), the high nibbles of 0..7 (r=2) / 8..15 (r=3);
+//   Q6_K: ql bytes h*64 + 32*(q%2) + kh*16 .. +15 and qh bytes
+//         128 + h*32 + kh*16 .. +15 hold quarter q of half h, elements
+//         h*128 + q*32 + kh*16 + 0..15; step t = 2q + u takes bytes 8u .. 8u+7.
+__device__ __forceinline__ constexpr uint32_t acol(int t) { return uint32_t((t >> 1) * 32 + (t & 1) * 8); }
 
-// Per-super-block factors of one row: Q4_K f[j] = d*sc_j, g[j] = dmin*mn_j
-// (j = 0..7); Q6_K f[j] = d*sc_j (j = 0..15).
+// The packed bytes of one super-block row that one lane consumes, loaded a
+// super-block ahead of their use.
 template <int FMT>
-struct BlkScale {
-    float f[FMT == kFmtQ4 ? 8 : 16];
-    float g[FMT == kFmtQ4 ? 8 : 1];
+struct WRaw;
+template <>
+struct WRaw<kFmtQ4> {
+    u32x4 hdr;    // d, dmin, 12 scale bytes
+    u32x4 qs[4];  // qs chunk c, bytes kh*16 .. +15
+};
+template <>
+struct WRaw<kFmtQ6> {
+    u32x4 v[7];      // 16-byte pieces read from the dword floor: ql h*64 + {0,32} + kh*16 (h = 0, 1),
+    uint32_t e[7];   // qh 128 + h*32 + kh*16, scales 192; e = the dword after each piece
+    uint32_t d;      // bytes 208..209
+    uint32_t sh;     // block address mod 4 (0 or 2: Q6_K blocks are 210 bytes)
+};
+
+// The same bytes ready for the element decode, with the per-step factors:
+// Q4_K f[j] = d*sc_j (odd j: times 1/16, as those steps convert 16*q),
+// g[j] = dmin*mn_j; Q6_K f[h*4 + q] = d*sc_{h*8 + 2q + kh}, this lane's
+// 16-element sub-block of quarter q.
+template <int FMT>
+struct WDec;
+template <>
+struct WDec<kFmtQ4> {
+    u32x4 qs[4];
+    float f[8], g[8];
+};
+template <>
+struct WDec<kFmtQ6> {
+    u32x4 ql[4], qh[2];
+    float f[8];
 };
 
 template <int FMT>
-__device__ __forceinline__ void load_scales(const uint8_t* blk, BlkScale<FMT>& s)
+__device__ __forceinline__ void load_w(const uint8_t* blk, uint32_t kh, WRaw<FMT>& r)
+{
+    if constexpr (FMT == kFmtQ4) {
+        r.hdr = *reinterpret_cast<const u32x4*>(blk);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) r.qs[c] = *reinterpret_cast<const u32x4*>(blk + 16 + c * 32 + kh * 16);
+    } else {
+        // every dword read lies inside the 210-byte block: a piece at offset o
+        // reads [o - sh, o - sh + 20) when sh = 2 and [o, o + 16) plus the
+        // dword at o + 12 when sh = 0
+        const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(blk)) & 3u;
+        const uint8_t* b = blk - sh;
+        const uint32_t eo = sh ? 16u : 12u;
+#pragma unroll
+        for (int i = 0; i < 7; ++i) {
+            const uint32_t o = i < 4 ? uint32_t(i) * 32u + kh * 16u : i < 6 ? 128u + uint32_t(i - 4) * 32u + kh * 16u : 192u;
+            r.v[i] = *reinterpret_cast<const u32x4a4*>(b + o);
+            r.e[i] = *reinterpret_cast<const uint32_t*>(b + o + eo);
+        }
+        r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
+        r.sh = sh;
+    }
+}
+
+template <int FMT>
+__device__ __forceinline__ void decode_w(const WRaw<FMT>& r, uint32_t kh, WDec<FMT>& w)
 {
 #pragma clang fp contract(off)
     if constexpr (FMT == kFmtQ4) {
-        const uint4 h = *reinterpret_cast<const uint4*>(blk);
-        const float d = f16_bits_to_f32(h.x), dmin = f16_bits_to_f32(h.x >> 16);
-        const uint32_t b[3] = {h.y, h.z, h.w};
+        const float d = f16_bits_to_f32(r.hdr.x), dmin = f16_bits_to_f32(r.hdr.x >> 16);
+        const uint32_t b[3] = {r.hdr.y, r.hdr.z, r.hdr.w};
         auto byte = [&](int i) { return (b[i >> 2] >> (8 * (i & 3))) & 0xffu; };
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -122,202 +174,285 @@ __device__ __forceinline__ void load_scales(const uint8_t* blk, BlkScale<FMT>& s
                 sc = (byte(j + 4) & 15u) | ((byte(j - 4) >> 6) << 4);
                 mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
             }
-            s.f[j] = d * float(sc);
-            s.g[j] = dmin * float(mn);
+            const float f = d * float(sc);
+            w.f[j] = (j & 1) ? f * 0.0625f : f;
+            w.g[j] = dmin * float(mn);
         }
-    } else {
-        uint32_t lo, hi, l2, h2;
-        ld8_2a(blk + 192, lo, hi);
-        ld8_2a(blk + 200, l2, h2);
-        const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 208));
-        const uint32_t sw[4] = {lo, hi, l2, h2};
 #pragma unroll
-        for (int j = 0; j < 16; ++j) s.f[j] = d * float(int8_t(uint8_t(sw[j >> 2] >> (8 * (j & 3)))));
-        s.g[0] = 0.0f;
+        for (int c = 0; c < 4; ++c) w.qs[c] = r.qs[c];
+        (void)kh;
+    } else {
+        u32x4 al[7];
+#pragma unroll
+        for (int i = 0; i < 7; ++i) {
+            al[i].x = __builtin_amdgcn_alignbyte(r.v[i].y, r.v[i].x, r.sh);
+            al[i].y = __builtin_amdgcn_alignbyte(r.v[i].z, r.v[i].y, r.sh);
+            al[i].z = __builtin_amdgcn_alignbyte(r.v[i].w, r.v[i].z, r.sh);
+            al[i].w = __builtin_amdgcn_alignbyte(r.e[i], r.v[i].w, r.sh);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w.ql[i] = al[i];
+        w.qh[0] = al[4];
+        w.qh[1] = al[5];
+        const float d = f16_bits_to_f32(r.d);
+        const uint32_t s = 8u * kh;
+        const uint32_t sw[4] = {al[6].x >> s, al[6].y >> s, al[6].z >> s, al[6].w >> s};
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                w.f[h * 4 + q] = d * float(int8_t(uint8_t(sw[h * 2 + (q >> 1)] >> (16 * (q & 1)))));
     }
 }
 
-// The 8 weights at elements hb*128 + KS*16 + kh*8 .. +7 of one super-block
-// row (hb: half block, KS: 16-wide K step, kh: lane half), as fp16, with the
-// element decode's fp32 arithmetic.  a / c are the factors of the element's
-// sub-block (Q4_K: d*sc, dmin*mn; Q6_K: d*sc), selected by the caller so no
-// register array is indexed at run time.
-template <int FMT, int KS>
-__device__ __forceinline__ half8 dequant8(const uint8_t* blk, uint32_t hb, uint32_t kh, float a, float c)
+// Step T of half HB: this lane's 8 weights as fp16, with the element
+// decode's fp32 arithmetic (Q4_K (d*sc)*q - dmin*mn, Q6_K (d*sc)*(q - 32)).
+template <int FMT, int HB, int T>
+__device__ __forceinline__ half8 dequant_step(const WDec<FMT>& w)
 {
 #pragma clang fp contract(off)
-    half8 w;
+    half8 o;
     if constexpr (FMT == kFmtQ4) {
-        // element e = hb*128 + KS*16 + kh*8: chunk byte 16 + (e>>6)*32 + (e&31), high nibble when e&32
-        const uint2 q = *reinterpret_cast<const uint2*>(blk + 16 + (hb * 2 + KS / 4) * 32 + (KS & 1) * 16 + kh * 8);
-        constexpr uint32_t sh = ((KS >> 1) & 1) ? 4u : 0u;
+        constexpr int c = HB * 2 + (T >> 2), r = T & 3, j = 2 * c + (r >> 1);
+        constexpr uint32_t mask = r < 2 ? 0x0f0f0f0fu : 0xf0f0f0f0u;
+        const uint32_t m0 = opaque(w.qs[c][(r & 1) * 2] & mask), m1 = opaque(w.qs[c][(r & 1) * 2 + 1] & mask);
+        const float a = w.f[j], cm = w.g[j];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t byte = ((i < 4 ? q.x : q.y) >> (8 * (i & 3))) & 0xffu;
-            const float b = a * float((byte >> sh) & 15u);
-            w[i] = _Float16(b - c);
+            const float b = a * byte_f(i < 4 ? m0 : m1, i & 3);
+            o[i] = _Float16(b - cm);
         }
     } else {
-        // half hb, quarter KS/2, l0 = (KS&1)*16 + kh*8
-        constexpr uint32_t quarter = KS >> 1;
-        const uint32_t l0 = (KS & 1) * 16 + kh * 8;
-        uint32_t ql0, ql1, qh0, qh1;
-        ld8_2a(blk + hb * 64 + l0 + 32 * (quarter & 1u), ql0, ql1);
-        ld8_2a(blk + 128 + hb * 32 + l0, qh0, qh1);
-        constexpr uint32_t lsh = (quarter >> 1) * 4u, hsh = quarter * 2u;
+        constexpr int q = T >> 1, u = T & 1;
+        constexpr uint32_t lsh = (q >> 1) * 4u, hsh = q * 2u;
+        const u32x4& l = w.ql[HB * 2 + (q & 1)];
+        const u32x4& hh = w.qh[HB];
+        const uint32_t c0 = ((l[2 * u] >> lsh) & 0x0f0f0f0fu) | (((hh[2 * u] >> hsh) & 0x03030303u) << 4);
+        const uint32_t c1 = ((l[2 * u + 1] >> lsh) & 0x0f0f0f0fu) | (((hh[2 * u + 1] >> hsh) & 0x03030303u) << 4);
+        const float a = w.f[HB * 4 + q];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t lb = ((i < 4 ? ql0 : ql1) >> (8 * (i & 3))) & 0xffu;
-            const uint32_t hbt = ((i < 4 ? qh0 : qh1) >> (8 * (i & 3))) & 0xffu;
-            const int code = int(((lb >> lsh) & 15u) | (((hbt >> hsh) & 3u) << 4)) - 32;
-            w[i] = _Float16(a * float(code));
-        }
-        (void)c;
+        for (int i = 0; i < 8; ++i) o[i] = _Float16(a * (byte_f(i < 4 ? c0 : c1, i & 3) - 32.0f));
     }
-    return w;
+    return o;
 }
 
 // X staging of one LDS stage: K columns [k0, k0+128) of rows [0, MB*32),
-// MB*32*16 pieces of 16 bytes, MB*2 per thread.
-template <int MB>
-__device__ __forceinline__ void x_fetch(const PfGemm& p, uint32_t k0, u32x4 (&reg)[MB * 2])
+// MB*32*16 pieces of 16 bytes, MB*2 per thread, moved in two parts of MB
+// pieces (part P: pieces P*MB .. P*MB + MB-1 of each thread).
+template <int MB, int P>
+__device__ __forceinline__ void x_fetch(const PfGemm& p, uint32_t k0, u32x4 (&reg)[MB])
 {
 #pragma unroll
-    for (int i = 0; i < MB * 2; ++i) {
-        const uint32_t c = threadIdx.x + 256u * uint32_t(i);
+    for (int i = 0; i < MB; ++i) {
+        const uint32_t c = threadIdx.x + 256u * uint32_t(P * MB + i);
         reg[i] = *reinterpret_cast<const u32x4*>(p.x + uint64_t(c >> 4) * p.ldx + k0 + (c & 15u) * 8);
     }
 }
 
-template <int MB>
-__device__ __forceinline__ void x_store(_Float16* stage, const u32x4 (&reg)[MB * 2])
+template <int MB, int P>
+__device__ __forceinline__ void x_store(_Float16* stage, const u32x4 (&reg)[MB])
 {
 #pragma unroll
-    for (int i = 0; i < MB * 2; ++i) {
-        const uint32_t c = threadIdx.x + 256u * uint32_t(i);
+    for (int i = 0; i < MB; ++i) {
+        const uint32_t c = threadIdx.x + 256u * uint32_t(P * MB + i);
         *reinterpret_cast<u32x4*>(stage + (c >> 4) * kPfLd + (c & 15u) * 8) = reg[i];
     }
 }
 
-// One 16-wide K step: this lane's B fragment, then MB MFMAs.
-template <int FMT, int MB, int HB, int KS>
-__device__ __forceinline__ void k_step(const uint8_t* blk, uint32_t kh, const BlkScale<FMT>& sc, const _Float16* a,
-                                       f32x16 (&acc)[MB])
+template <int MB>
+__device__ __forceinline__ void load_a(const _Float16* a, half8 (&f)[MB])
 {
-    // sub-block factors of elements HB*128 + KS*16 + kh*8 .. +7
-    constexpr int F = FMT == kFmtQ4 ? HB * 4 + KS / 2 : HB * 8 + KS;
-    const float fc = FMT == kFmtQ4 ? sc.g[F < 8 ? F : 0] : 0.0f;
-    const half8 b = dequant8<FMT, KS>(blk, HB, kh, sc.f[F], fc);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) f[mb] = *reinterpret_cast<const half8*>(a + mb * 32 * kPfLd);
+}
+
+// Workgroup barrier ordering LDS only: global loads in flight (the next
+// super-block's weights, the next X stage) stay in flight across it.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Per-lane state of the GEMM pipeline: NF B fragments (weight rows) per
+// lane against MB A fragments (32-row blocks of X).
+template <int FMT, int MB, int NF>
+struct PfState {
+    f32x16 acc[NF][MB];
+    half8 af[MB];          // A fragments of the step being issued
+    WDec<FMT> dec[NF];     // the current super-block, decoded
+    WRaw<FMT> raw[NF];     // the next super-block, as loaded
+};
+
+// Step T of half HB.  The NF*MB MFMAs of this step (B fragments `bc`, A
+// fragments in s.af) issue one A block at a time; right behind each block's
+// MFMAs its A fragment for step T+1 is read from LDS into the same registers,
+// and the B fragments of the next step are decoded into `bn` in between.  At
+// T = 7 the next step is step 0 of the next half: half 1 of this super-block,
+// or, once s.raw is decoded into s.dec, half 0 of the next super-block (its A
+// fragments are read after the barrier).  The sched_group_barrier pattern
+// keeps MFMA, LDS read and VALU interleaved so one wave per SIMD keeps the
+// matrix pipe busy.
+template <int FMT, int MB, int NF, int HB, int T>
+__device__ __forceinline__ void pf_step(PfState<FMT, MB, NF>& s, const _Float16* a, uint32_t kh, const half8 (&bc)[NF],
+                                        half8 (&bn)[NF])
+{
+    constexpr bool kNextSb = T == 7 && HB == 1;
+    if constexpr (kNextSb) {
+#pragma unroll
+        for (int j = 0; j < NF; ++j) decode_w<FMT>(s.raw[j], kh, s.dec[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < NF; ++j) bn[j] = dequant_step<FMT, (T == 7 ? 1 - HB : HB), (T + 1) & 7>(s.dec[j]);
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-        const half8 av = *reinterpret_cast<const half8*>(a + mb * 32 * kPfLd + KS * 16);
-        acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, b, acc[mb], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < NF; ++j)
+            s.acc[j][mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(s.af[mb], bc[j], s.acc[j][mb], 0, 0, 0);
+        if constexpr (T < 7) s.af[mb] = *reinterpret_cast<const half8*>(a + acol(T + 1) + mb * 32 * kPfLd);
     }
+    constexpr int kValu = ((kNextSb ? 110 : 34) * NF + MB - 1) / MB;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        __builtin_amdgcn_sched_group_barrier(0x008, NF, 0);  // MFMA
+        if constexpr (T < 7) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);  // VALU
+    }
+    __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int FMT, int MB, int HB>
-__device__ __forceinline__ void half_block(const uint8_t* blk, uint32_t kh, const BlkScale<FMT>& sc, const _Float16* a,
-                                           f32x16 (&acc)[MB])
+// One half super-block of MFMAs from LDS stage `a`, while the other stage
+// (not read during this half) is filled with K columns [xk0, xk0+128) of X
+// in two parts.  Half 1 also issues the weight loads of the next super-block
+// (after the first X part, so that waiting for X never waits for them); they
+// are decoded in its last step.  b0 holds the B fragments of step 0 on entry
+// and of the next half's step 0 on exit.
+template <int FMT, int MB, int NF, int HB>
+__device__ __forceinline__ void pf_half(const PfGemm& p, PfState<FMT, MB, NF>& s, const _Float16* a, uint32_t xk0,
+                                        _Float16* xdst, const uint8_t* const (&wnext)[NF], uint32_t kh,
+                                        half8 (&b0)[NF], half8 (&b1)[NF])
 {
-    k_step<FMT, MB, HB, 0>(blk, kh, sc, a, acc);
-    k_step<FMT, MB, HB, 1>(blk, kh, sc, a, acc);
-    k_step<FMT, MB, HB, 2>(blk, kh, sc, a, acc);
-    k_step<FMT, MB, HB, 3>(blk, kh, sc, a, acc);
-    k_step<FMT, MB, HB, 4>(blk, kh, sc, a, acc);
-    k_step<FMT, MB, HB, 5>(blk, kh, sc, a, acc);
-    k_step<FMT, MB, HB, 6>(blk, kh, sc, a, acc);
-    k_step<FMT, MB, HB, 7>(blk, kh, sc, a, acc);
+    u32x4 xr[MB];
+    x_fetch<MB, 0>(p, xk0, xr);
+    if constexpr (HB == 1) {
+#pragma unroll
+        for (int j = 0; j < NF; ++j) load_w<FMT>(wnext[j], kh, s.raw[j]);
+    }
+    load_a<MB>(a, s.af);
+    __builtin_amdgcn_sched_barrier(0);
+    pf_step<FMT, MB, NF, HB, 0>(s, a, kh, b0, b1);
+    pf_step<FMT, MB, NF, HB, 1>(s, a, kh, b1, b0);
+    pf_step<FMT, MB, NF, HB, 2>(s, a, kh, b0, b1);
+    pf_step<FMT, MB, NF, HB, 3>(s, a, kh, b1, b0);
+    x_store<MB, 0>(xdst, xr);
+    x_fetch<MB, 1>(p, xk0, xr);
+    __builtin_amdgcn_sched_barrier(0);
+    pf_step<FMT, MB, NF, HB, 4>(s, a, kh, b0, b1);
+    pf_step<FMT, MB, NF, HB, 5>(s, a, kh, b1, b0);
+    pf_step<FMT, MB, NF, HB, 6>(s, a, kh, b0, b1);
+    pf_step<FMT, MB, NF, HB, 7>(s, a, kh, b1, b0);
+    x_store<MB, 1>(xdst, xr);
 }
 
-template <int FMT, int MB, bool SWIGLU>
+// Y = X W^T over super-blocks [kb0, kb1) of K for MB*32 rows of X.
+// Workgroup: 4 waves, one per SIMD; lane (l%32) of wave w owns weight row(s)
+//   SWIGLU (NF = 2): gate and up row c = blockIdx.x*128 + w*32 + l%32, and
+//                    writes s[m][c] = silu(X Wg^T)[m][c] * (X Wu^T)[m][c];
+//   PLAIN:           rows c_j = blockIdx.x*128*NF + w*32*NF + j*32 + l%32
+//                    (row c < ncol0 from w0, else row c - ncol0 of w1), and
+//                    writes split partials out[blockIdx.y][m][c].
+// X is staged in LDS half a super-block (128 K columns) at a time, double-
+// buffered; the weights of super-block kb+1 are loaded during kb.
+template <int FMT, int MB, int NF, bool SWIGLU>
 __global__ __launch_bounds__(256, 1) void k_pf_gemm(PfGemm p)
 {
+    static_assert(!SWIGLU || NF == 2, "SwiGLU pairs a gate and an up row per lane");
     extern __shared__ _Float16 ash[];  // [2][MB*32][kPfLd]
-    constexpr int kRows = MB * 32;
-    constexpr int kStage = kRows * kPfLd;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-
-    // this lane's weight row (B column) and output column
-    uint32_t col;
-    const uint8_t* wrow;
-    if constexpr (SWIGLU) {
-        col = blockIdx.x * 64 + (wave & 1) * 32 + (lane & 31);
-        const uint32_t r = min(col, p.N - 1);
-        wrow = (wave < 2 ? p.w0 : p.w1) + uint64_t(r) * p.row_bytes;
-    } else {
-        col = blockIdx.x * 128 + wave * 32 + (lane & 31);
-        const uint32_t r = min(col, p.N - 1);
-        wrow = r < p.ncol0 ? p.w0 + uint64_t(r) * p.row_bytes : p.w1 + uint64_t(r - p.ncol0) * p.row_bytes;
-    }
+    constexpr int kStage = MB * 32 * kPfLd;
     constexpr int kBB = FMT == kFmtQ4 ? kQ4Bytes : kQ6Bytes;
-    const uint32_t kb0 = blockIdx.y * p.bps, kb1 = min(p.nb, kb0 + p.bps);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t kh = uint32_t(lane) >> 5;
 
-    f32x16 acc[MB];
+    uint32_t col[NF];
+    const uint8_t* wrow[NF];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[mb][i] = 0.0f;
+    for (int j = 0; j < NF; ++j) {
+        if constexpr (SWIGLU) {
+            col[j] = blockIdx.x * 128 + wave * 32 + (lane & 31);
+            wrow[j] = (j == 0 ? p.w0 : p.w1) + uint64_t(min(col[j], p.N - 1)) * p.row_bytes;
+        } else {
+            col[j] = blockIdx.x * (128 * NF) + wave * (32 * NF) + j * 32 + (lane & 31);
+            const uint32_t r = min(col[j], p.N - 1);
+            wrow[j] = r < p.ncol0 ? p.w0 + uint64_t(r) * p.row_bytes : p.w1 + uint64_t(r - p.ncol0) * p.row_bytes;
+        }
+    }
+    const uint32_t kb0 = blockIdx.y * p.bps, kb1 = min(p.nb, kb0 + p.bps);
 
-    // stage 0 holds the first half of the current super-block, stage 1 the
-    // second; each half's compute overlaps the fetch of the next half, whose
-    // LDS store follows a barrier (the last fetch repeats the last half).
-    u32x4 reg[MB * 2];
-    x_fetch<MB>(p, kb0 * kQK, reg);
-    x_store<MB>(ash, reg);
-    __syncthreads();
-    const _Float16* a0 = ash + (lane & 31) * kPfLd + kh * 8;
+    PfState<FMT, MB, NF> s;
+#pragma unroll
+    for (int j = 0; j < NF; ++j)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s.acc[j][mb][i] = 0.0f;
+
+    // prologue: weights of kb0, stage 0 = half 0 of kb0
+#pragma unroll
+    for (int j = 0; j < NF; ++j) load_w<FMT>(wrow[j] + uint64_t(kb0) * kBB, kh, s.raw[j]);
+    {
+        u32x4 xr[MB];
+        x_fetch<MB, 0>(p, kb0 * kQK, xr);
+        x_store<MB, 0>(ash, xr);
+        x_fetch<MB, 1>(p, kb0 * kQK, xr);
+        x_store<MB, 1>(ash, xr);
+    }
+    half8 b0[NF], b1[NF];
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+        decode_w<FMT>(s.raw[j], kh, s.dec[j]);
+        b0[j] = dequant_step<FMT, 0, 0>(s.dec[j]);
+    }
+    lds_barrier();
+    const _Float16* a0 = ash + (lane & 31) * kPfLd + kh * 16;
     const _Float16* a1 = a0 + kStage;
     for (uint32_t kb = kb0; kb < kb1; ++kb) {
-        const uint8_t* blk = wrow + uint64_t(kb) * kBB;
-        BlkScale<FMT> sc;
-        load_scales<FMT>(blk, sc);
-        x_fetch<MB>(p, kb * kQK + kPfKT, reg);
-        half_block<FMT, MB, 0>(blk, kh, sc, a0, acc);
-        x_store<MB>(ash + kStage, reg);
-        __syncthreads();
-        const uint32_t nk = kb + 1 < kb1 ? kb + 1 : kb;
-        x_fetch<MB>(p, nk * kQK, reg);
-        half_block<FMT, MB, 1>(blk, kh, sc, a1, acc);
-        __syncthreads();
-        x_store<MB>(ash, reg);
-        __syncthreads();
+        // the last super-block of the range re-loads and re-stages itself
+        const uint32_t kn = kb + 1 < kb1 ? kb + 1 : kb;
+        const uint8_t* wn[NF];
+#pragma unroll
+        for (int j = 0; j < NF; ++j) wn[j] = wrow[j] + uint64_t(kn) * kBB;
+        pf_half<FMT, MB, NF, 0>(p, s, a0, kb * kQK + kPfKT, ash + kStage, wn, kh, b0, b1);
+        lds_barrier();
+        pf_half<FMT, MB, NF, 1>(p, s, a1, kn * kQK, ash, wn, kh, b0, b1);
+        lds_barrier();
     }
 
-    // D[m][col]: register i of block mb holds row mb*32 + (i/4)*8 + (lane/32)*4 + i%4
+    // D[m][c]: register i of block mb holds row mb*32 + (i/4)*8 + (lane/32)*4 + i%4
     if constexpr (SWIGLU) {
-        float* u = reinterpret_cast<float*>(ash);  // [kRows][64], after the last sync
-        if (wave >= 2) {
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int m = mb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-                    u[m * 64 + (wave & 1) * 32 + (lane & 31)] = acc[mb][i];
-                }
-        }
-        __syncthreads();
-        if (wave < 2 && col < p.N) {
+        if (col[0] < p.N) {
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const uint32_t m = mb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
                     if (m < p.M) {
-                        const float g = acc[mb][i], uv = u[m * 64 + (wave & 1) * 32 + (lane & 31)];
-                        p.s[uint64_t(m) * p.lds_out + col] = _Float16((g / (1.0f + expf(-g))) * uv);
+                        const float g = s.acc[0][mb][i], u = s.acc[1][mb][i];
+                        p.s[uint64_t(m) * p.lds_out + col[0]] = _Float16((g / (1.0f + expf(-g))) * u);
                     }
                 }
         }
     } else {
-        if (col < p.N) {
-            float* o = p.out + uint64_t(blockIdx.y) * p.mpad * p.N + col;
+#pragma unroll
+        for (int j = 0; j < NF; ++j) {
+            if (col[j] >= p.N) continue;
+            float* o = p.out + uint64_t(blockIdx.y) * p.mpad * p.N + col[j];
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const uint32_t m = mb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-                    if (m < p.M) o[uint64_t(m) * p.N] = acc[mb][i];
+                    if (m < p.M) o[uint64_t(m) * p.N] = s.acc[j][mb][i];
                 }
         }
     }
@@ -538,29 +673,29 @@ namespace {
 
 constexpr uint32_t kPfTargetWgs = 256;
 
-template <int FMT, int MB, bool SW>
+template <int FMT, int MB, int NF, bool SW>
 hipError_t launch_gemm_t(const PfGemm& p, uint32_t gx, uint32_t splits, hipStream_t st)
 {
     const size_t lds = size_t(2) * MB * 32 * kPfLd * sizeof(_Float16);
     static bool attr = false;
     if (!attr) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm<FMT, MB, SW>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm<FMT, MB, NF, SW>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL((k_pf_gemm<FMT, MB, SW>), dim3(gx, splits), dim3(256), lds, st, p);
+    hipLaunchKernelGGL((k_pf_gemm<FMT, MB, NF, SW>), dim3(gx, splits), dim3(256), lds, st, p);
     return hipGetLastError();
 }
 
-template <int FMT, bool SW>
+template <int FMT, int NF, bool SW>
 hipError_t launch_gemm_mb(const PfGemm& p, uint32_t mb, uint32_t gx, uint32_t splits, hipStream_t st)
 {
     switch (mb) {
-    case 1: return launch_gemm_t<FMT, 1, SW>(p, gx, splits, st);
-    case 2: return launch_gemm_t<FMT, 2, SW>(p, gx, splits, st);
-    case 4: return launch_gemm_t<FMT, 4, SW>(p, gx, splits, st);
-    default: return launch_gemm_t<FMT, 8, SW>(p, gx, splits, st);
+    case 1: return launch_gemm_t<FMT, 1, NF, SW>(p, gx, splits, st);
+    case 2: return launch_gemm_t<FMT, 2, NF, SW>(p, gx, splits, st);
+    case 4: return launch_gemm_t<FMT, 4, NF, SW>(p, gx, splits, st);
+    default: return launch_gemm_t<FMT, 8, NF, SW>(p, gx, splits, st);
     }
 }
 
@@ -570,14 +705,23 @@ uint32_t m_blocks(uint32_t M)
     return b <= 1 ? 1 : b <= 2 ? 2 : b <= 4 ? 4 : 8;
 }
 
-// Split-K plan of a PLAIN projection: enough workgroups to cover the CUs.
+// Split-K plan of a PLAIN projection (NF = 1, 128 columns per workgroup):
+// the split count whose super-blocks per workgroup times rounds of
+// workgroups over the CUs (one resident workgroup per CU) is smallest, the
+// fewest splits (least partial traffic) among equals.
 void split_plan(uint32_t N, uint32_t nb, uint32_t& gx, uint32_t& splits, uint32_t& bps)
 {
     gx = (N + 127) / 128;
-    uint32_t want = (kPfTargetWgs + gx - 1) / gx;
-    want = std::max(1u, std::min(want, nb));
-    bps = (nb + want - 1) / want;
-    splits = (nb + bps - 1) / bps;
+    uint32_t best = ~0u;
+    for (uint32_t want = 1; want <= nb; ++want) {
+        const uint32_t b = (nb + want - 1) / want, sp = (nb + b - 1) / b;
+        const uint32_t rounds = (gx * sp + kPfTargetWgs - 1) / kPfTargetWgs;
+        if (b * rounds < best) {
+            best = b * rounds;
+            bps = b;
+            splits = sp;
+        }
+    }
 }
 
 template <int H>
@@ -713,7 +857,7 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             g.N = H + kvd;
             split_plan(g.N, g.nb, gx, sp, bps);
             g.bps = bps;
-            if ((rc = chk(launch_gemm_mb<kFmtQ4, false>(g, mb, gx, sp, st), "q/k projection"))) return rc;
+            if ((rc = chk(launch_gemm_mb<kFmtQ4, 1, false>(g, mb, gx, sp, st), "q/k projection"))) return rc;
             hipLaunchKernelGGL(k_pf_qk_epi, dim3((g.N / 2 + 255) / 256, M), dim3(256), 0, st, pf->part, sp,
                                uint32_t(kPfMaxM), H, kvd, L.qb, L.kb, S->rope, p0, pf->q, kc);
             if ((rc = chk(hipGetLastError(), "q/k epilogue"))) return rc;
@@ -724,8 +868,8 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             g.N = kvd;
             split_plan(g.N, g.nb, gx, sp, bps);
             g.bps = bps;
-            rc = chk(L.v_type == kFmtQ4 ? launch_gemm_mb<kFmtQ4, false>(g, mb, gx, sp, st)
-                                        : launch_gemm_mb<kFmtQ6, false>(g, mb, gx, sp, st),
+            rc = chk(L.v_type == kFmtQ4 ? launch_gemm_mb<kFmtQ4, 1, false>(g, mb, gx, sp, st)
+                                        : launch_gemm_mb<kFmtQ6, 1, false>(g, mb, gx, sp, st),
                      "v projection");
             if (rc) return rc;
             hipLaunchKernelGGL(k_pf_v_epi, dim3((kvd + 255) / 256, M), dim3(256), 0, st, pf->part, sp,
@@ -741,7 +885,7 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             g.N = H;
             split_plan(g.N, g.nb, gx, sp, bps);
             g.bps = bps;
-            if ((rc = chk(launch_gemm_mb<kFmtQ4, false>(g, mb, gx, sp, st), "o projection"))) return rc;
+            if ((rc = chk(launch_gemm_mb<kFmtQ4, 1, false>(g, mb, gx, sp, st), "o projection"))) return rc;
             hipLaunchKernelGGL(k_pf_res_epi, dim3((H + 255) / 256, M), dim3(256), 0, st, pf->part, sp,
                                uint32_t(kPfMaxM), H, pf->h);
             if ((rc = chk(hipGetLastError(), "o residual"))) return rc;
@@ -757,7 +901,7 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             u.bps = g.nb;
             u.s = pf->xs;
             u.lds_out = F;
-            if ((rc = chk(launch_gemm_mb<kFmtQ4, true>(u, mb, (F + 63) / 64, 1, st), "gate/up"))) return rc;
+            if ((rc = chk(launch_gemm_mb<kFmtQ4, 2, true>(u, mb, (F + 127) / 128, 1, st), "gate/up"))) return rc;
             // down + residual
             PfGemm dn = g;
             dn.x = pf->xs;
@@ -769,8 +913,8 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             dn.N = H;
             split_plan(dn.N, dn.nb, gx, sp, bps);
             dn.bps = bps;
-            rc = chk(L.down_type == kFmtQ4 ? launch_gemm_mb<kFmtQ4, false>(dn, mb, gx, sp, st)
-                                           : launch_gemm_mb<kFmtQ6, false>(dn, mb, gx, sp, st),
+            rc = chk(L.down_type == kFmtQ4 ? launch_gemm_mb<kFmtQ4, 1, false>(dn, mb, gx, sp, st)
+                                           : launch_gemm_mb<kFmtQ6, 1, false>(dn, mb, gx, sp, st),
                      "down projection");
             if (rc) return rc;
             hipLaunchKernelGGL(k_pf_res_epi, dim3((H + 255) / 256, M), dim3(256), 0, st, pf->part, sp,

@@ -114,7 +114,7 @@ def decode_leg(steps: int, warmup: int, graph: bool = True) -> dict:
     wbytes = model.weight_bytes
     kvd = d.kv_heads * d.head_dim
     ctxs = (512, 2048, 4096)
-    sess = arc.Session(model, max(ctxs) + steps)
+    sess = arc.Session(model, max(ctxs) + max(steps, warmup, 1))
     out = {"model": "Qwen2.5-7B shape, 28 layers, Q4_K_M layout, random init",
            "launch": "captured graph, one replay per token" if graph else "kernel-by-kernel launches",
            "weight_bytes": wbytes, "steps": steps, "kernels_per_step": None, "contexts": {}}
