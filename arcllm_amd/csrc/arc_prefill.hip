@@ -114,10 +114,11 @@ struct WRaw<kFmtQ6> {
     uint32_t sh;     // block address mod 4 (0 or 2: Q6_K blocks are 210 bytes)
 };
 
-// The same bytes ready for the element decode, with the per-step factors:
-// Q4_K f[j] = d*sc_j (odd j: times 1/16, as those steps convert 16*q),
-// g[j] = dmin*mn_j; Q6_K f[h*4 + q] = d*sc_{h*8 + 2q + kh}, this lane's
-// 16-element sub-block of quarter q.
+// The same bytes ready for the element decode, with the per-step factors
+// (codes are read as fp16 subnormals, q * 2^-24, so the factor carries
+// 2^24): Q4_K f[j] = d*sc_j * 2^24 (odd j: 2^20, as those steps read 16*q),
+// g[j] = -dmin*mn_j; Q6_K f[h*4 + q] = d*sc * 2^24 and n = -32*d*sc for
+// sc = sc_{h*8 + 2q + kh}, this lane's 16-element sub-block of quarter q.
 template <int FMT>
 struct WDec;
 template <>
@@ -128,7 +129,7 @@ struct WDec<kFmtQ4> {
 template <>
 struct WDec<kFmtQ6> {
     u32x4 ql[4], qh[2];
-    float f[8];
+    float f[8], n[8];
 };
 
 template <int FMT>
@@ -162,6 +163,7 @@ __device__ __forceinline__ void decode_w(const WRaw<FMT>& r, uint32_t kh, WDec<F
 #pragma clang fp contract(off)
     if constexpr (FMT == kFmtQ4) {
         const float d = f16_bits_to_f32(r.hdr.x), dmin = f16_bits_to_f32(r.hdr.x >> 16);
+        const float d24 = d * 16777216.0f, d20 = d * 1048576.0f;  // exact
         const uint32_t b[3] = {r.hdr.y, r.hdr.z, r.hdr.w};
         auto byte = [&](int i) { return (b[i >> 2] >> (8 * (i & 3))) & 0xffu; };
 #pragma unroll
@@ -174,9 +176,8 @@ __device__ __forceinline__ void decode_w(const WRaw<FMT>& r, uint32_t kh, WDec<F
                 sc = (byte(j + 4) & 15u) | ((byte(j - 4) >> 6) << 4);
                 mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
             }
-            const float f = d * float(sc);
-            w.f[j] = (j & 1) ? f * 0.0625f : f;
-            w.g[j] = dmin * float(mn);
+            w.f[j] = ((j & 1) ? d20 : d24) * float(sc);
+            w.g[j] = -(dmin * float(mn));
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) w.qs[c] = r.qs[c];
@@ -201,27 +202,55 @@ __device__ __forceinline__ void decode_w(const WRaw<FMT>& r, uint32_t kh, WDec<F
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                w.f[h * 4 + q] = d * float(int8_t(uint8_t(sw[h * 2 + (q >> 1)] >> (16 * (q & 1)))));
+            {
+                const float f = d * float(int8_t(uint8_t(sw[h * 2 + (q >> 1)] >> (16 * (q & 1)))));
+                w.f[h * 4 + q] = f * 16777216.0f;
+                w.n[h * 4 + q] = f * -32.0f;
+            }
     }
 }
 
-// Step T of half HB: this lane's 8 weights as fp16, with the element
-// decode's fp32 arithmetic (Q4_K (d*sc)*q - dmin*mn, Q6_K (d*sc)*(q - 32)).
+// Two codes held in the low bits of the fp16 halves of `pair` read as exact
+// subnormals (bits c -> c * 2^-24); fmaf(code * 2^-24, A, n) with A the
+// element factor times 2^24 is v_fma_mix.
+__device__ __forceinline__ float mixc(uint32_t pair, bool hi, float A, float n)
+{
+    const half2_t h = __builtin_bit_cast(half2_t, pair);
+    return __builtin_fmaf(static_cast<float>(hi ? h.y : h.x), A, n);
+}
+
+// Four weights from the four bytes of `codes` (each code < 2^10, in the low
+// bits of its byte or, for Q4_K high nibbles, times 16): bytes 0 and 2 are
+// the halves of codes & 0x00ff00ff, bytes 1 and 3 moved down by v_perm_b32.
+__device__ __forceinline__ void mix4w(uint32_t codes, float A, float n, half8& o, int at)
+{
+    const uint32_t ev = opaque(codes & 0x00ff00ffu);
+    const uint32_t od = opaque(__builtin_amdgcn_perm(0u, codes, 0x0c030c01u));  // [b1, 0, b3, 0]
+    o[at + 0] = _Float16(mixc(ev, false, A, n));
+    o[at + 1] = _Float16(mixc(od, false, A, n));
+    o[at + 2] = _Float16(mixc(ev, true, A, n));
+    o[at + 3] = _Float16(mixc(od, true, A, n));
+}
+
+// Step T of half HB: this lane's 8 weights as fp16, decoded in fp32 as one
+// fused multiply-add per element on the code read as an fp16 subnormal:
+// Q4_K fmaf(q * 2^-24, d*sc * 2^24, -dmin*mn) (high nibbles: 16q * 2^-24
+// against d*sc * 2^20), Q6_K fmaf((q+32) * 2^-24, d*sc * 2^24, -32*d*sc)
+// with q+32 the stored 6-bit code.  The scalings by powers of two are exact,
+// and both equal the element decode's (d*sc)*q - dmin*mn and (d*sc)*(q-32)
+// bit for bit: d has 11 significant bits, sc at most 6 (Q4_K) or 7 (Q6_K)
+// and q at most 4 or 6, so the product is exact in fp32 and only the final
+// add rounds.
 template <int FMT, int HB, int T>
 __device__ __forceinline__ half8 dequant_step(const WDec<FMT>& w)
 {
-#pragma clang fp contract(off)
     half8 o;
     if constexpr (FMT == kFmtQ4) {
         constexpr int c = HB * 2 + (T >> 2), r = T & 3, j = 2 * c + (r >> 1);
         constexpr uint32_t mask = r < 2 ? 0x0f0f0f0fu : 0xf0f0f0f0u;
-        const uint32_t m0 = opaque(w.qs[c][(r & 1) * 2] & mask), m1 = opaque(w.qs[c][(r & 1) * 2 + 1] & mask);
-        const float a = w.f[j], cm = w.g[j];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float b = a * byte_f(i < 4 ? m0 : m1, i & 3);
-            o[i] = _Float16(b - cm);
-        }
+        const float A = w.f[j], n = w.g[j];
+        mix4w(w.qs[c][(r & 1) * 2] & mask, A, n, o, 0);
+        mix4w(w.qs[c][(r & 1) * 2 + 1] & mask, A, n, o, 4);
     } else {
         constexpr int q = T >> 1, u = T & 1;
         constexpr uint32_t lsh = (q >> 1) * 4u, hsh = q * 2u;
@@ -229,34 +258,42 @@ __device__ __forceinline__ half8 dequant_step(const WDec<FMT>& w)
         const u32x4& hh = w.qh[HB];
         const uint32_t c0 = ((l[2 * u] >> lsh) & 0x0f0f0f0fu) | (((hh[2 * u] >> hsh) & 0x03030303u) << 4);
         const uint32_t c1 = ((l[2 * u + 1] >> lsh) & 0x0f0f0f0fu) | (((hh[2 * u + 1] >> hsh) & 0x03030303u) << 4);
-        const float a = w.f[HB * 4 + q];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = _Float16(a * (byte_f(i < 4 ? c0 : c1, i & 3) - 32.0f));
+        const float A = w.f[HB * 4 + q], n = w.n[HB * 4 + q];
+        mix4w(c0, A, n, o, 0);
+        mix4w(c1, A, n, o, 4);
     }
     return o;
 }
 
 // X staging of one LDS stage: K columns [k0, k0+128) of rows [0, MB*32),
 // MB*32*16 pieces of 16 bytes, MB*2 per thread, moved in two parts of MB
-// pieces (part P: pieces P*MB .. P*MB + MB-1 of each thread).
+// pieces (part P: pieces P*MB .. P*MB + MB-1 of each thread).  Piece i of a
+// thread is row (tid/16) + 16*i, columns (tid%16)*8 .. +7: the global loads
+// are buffer loads with the lane's byte offset `voff` and the uniform row and
+// column offset in a scalar register; the LDS stores use one base and
+// immediate offsets.
+struct XSrc {
+    __amdgpu_buffer_rsrc_t rsrc;  // X, MB*32 rows of ldx fp16
+    uint32_t voff;                // ((tid/16)*ldx + (tid%16)*8) * 2
+    uint32_t ldx;
+};
+
 template <int MB, int P>
-__device__ __forceinline__ void x_fetch(const PfGemm& p, uint32_t k0, u32x4 (&reg)[MB])
+__device__ __forceinline__ void x_fetch(const XSrc& xs, uint32_t k0, u32x4 (&reg)[MB])
 {
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
-        const uint32_t c = threadIdx.x + 256u * uint32_t(P * MB + i);
-        reg[i] = *reinterpret_cast<const u32x4*>(p.x + uint64_t(c >> 4) * p.ldx + k0 + (c & 15u) * 8);
+        const uint32_t soff = (16u * uint32_t(P * MB + i) * xs.ldx + k0) * 2u;
+        reg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xs.rsrc, xs.voff, soff, 0));
     }
 }
 
 template <int MB, int P>
 __device__ __forceinline__ void x_store(_Float16* stage, const u32x4 (&reg)[MB])
 {
+    _Float16* base = stage + (P * MB * 16) * kPfLd + (threadIdx.x >> 4) * kPfLd + (threadIdx.x & 15u) * 8u;
 #pragma unroll
-    for (int i = 0; i < MB; ++i) {
-        const uint32_t c = threadIdx.x + 256u * uint32_t(P * MB + i);
-        *reinterpret_cast<u32x4*>(stage + (c >> 4) * kPfLd + (c & 15u) * 8) = reg[i];
-    }
+    for (int i = 0; i < MB; ++i) *reinterpret_cast<u32x4*>(base + i * 16 * kPfLd) = reg[i];
 }
 
 template <int MB>
@@ -329,7 +366,7 @@ __device__ __forceinline__ void pf_step(PfState<FMT, MB, NF>& s, const _Float16*
 // are decoded in its last step.  b0 holds the B fragments of step 0 on entry
 // and of the next half's step 0 on exit.
 template <int FMT, int MB, int NF, int HB>
-__device__ __forceinline__ void pf_half(const PfGemm& p, PfState<FMT, MB, NF>& s, const _Float16* a, uint32_t xk0,
+__device__ __forceinline__ void pf_half(const XSrc& p, PfState<FMT, MB, NF>& s, const _Float16* a, uint32_t xk0,
                                         _Float16* xdst, const uint8_t* const (&wnext)[NF], uint32_t kh,
                                         half8 (&b0)[NF], half8 (&b1)[NF])
 {
@@ -397,14 +434,20 @@ __global__ __launch_bounds__(256, 1) void k_pf_gemm(PfGemm p)
 #pragma unroll
             for (int i = 0; i < 16; ++i) s.acc[j][mb][i] = 0.0f;
 
+    XSrc xs;
+    xs.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(p.x), (short)0, int(MB * 32 * p.ldx * 2u),
+                                                0x00020000);
+    xs.voff = ((uint32_t(tid) >> 4) * p.ldx + (uint32_t(tid) & 15u) * 8u) * 2u;
+    xs.ldx = p.ldx;
+
     // prologue: weights of kb0, stage 0 = half 0 of kb0
 #pragma unroll
     for (int j = 0; j < NF; ++j) load_w<FMT>(wrow[j] + uint64_t(kb0) * kBB, kh, s.raw[j]);
     {
         u32x4 xr[MB];
-        x_fetch<MB, 0>(p, kb0 * kQK, xr);
+        x_fetch<MB, 0>(xs, kb0 * kQK, xr);
         x_store<MB, 0>(ash, xr);
-        x_fetch<MB, 1>(p, kb0 * kQK, xr);
+        x_fetch<MB, 1>(xs, kb0 * kQK, xr);
         x_store<MB, 1>(ash, xr);
     }
     half8 b0[NF], b1[NF];
@@ -414,17 +457,20 @@ __global__ __launch_bounds__(256, 1) void k_pf_gemm(PfGemm p)
         b0[j] = dequant_step<FMT, 0, 0>(s.dec[j]);
     }
     lds_barrier();
-    const _Float16* a0 = ash + (lane & 31) * kPfLd + kh * 16;
-    const _Float16* a1 = a0 + kStage;
+    // stage 1's A base is a separate register (its offsets from stage 0 exceed
+    // the 16-bit LDS immediate)
+    const uint32_t ao = (lane & 31) * kPfLd + kh * 16;
+    const _Float16* a0 = ash + ao;
+    const _Float16* a1 = ash + opaque(ao + kStage);
     for (uint32_t kb = kb0; kb < kb1; ++kb) {
         // the last super-block of the range re-loads and re-stages itself
         const uint32_t kn = kb + 1 < kb1 ? kb + 1 : kb;
         const uint8_t* wn[NF];
 #pragma unroll
         for (int j = 0; j < NF; ++j) wn[j] = wrow[j] + uint64_t(kn) * kBB;
-        pf_half<FMT, MB, NF, 0>(p, s, a0, kb * kQK + kPfKT, ash + kStage, wn, kh, b0, b1);
+        pf_half<FMT, MB, NF, 0>(xs, s, a0, kb * kQK + kPfKT, ash + kStage, wn, kh, b0, b1);
         lds_barrier();
-        pf_half<FMT, MB, NF, 1>(p, s, a1, kn * kQK, ash, wn, kh, b0, b1);
+        pf_half<FMT, MB, NF, 1>(xs, s, a1, kn * kQK, ash, wn, kh, b0, b1);
         lds_barrier();
     }
 

@@ -100,3 +100,37 @@ def test_f16_gemv_is_exact_products_of_rounded_operands():
         np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12 * np.abs(ref).max())
         # and it differs from the exact-operand product (the rounding is real)
         assert not np.array_equal(got, orc.gemv_r64_xd(qt, w, rows, K, x))
+
+
+@pytest.mark.parametrize("qtype", [arc.Q4_K, arc.Q6_K])
+def test_element_products_are_exact_in_fp32(qtype):
+    """The batched prompt pass decodes weights as fmaf(d*sc, q, -dmin*mn)
+    (Q4_K) and fmaf(d*sc, q+32, -32*d*sc) (Q6_K); both equal the element
+    decode's separate multiply and subtract bit for bit because the product
+    d*sc*q is exact in binary32: d has 11 significant bits, sc at most 6
+    (Q4_K) or 7 (Q6_K) and q at most 4 (Q4_K) or 6 (Q6_K), so only the final
+    subtraction rounds.  Checked here on every element of random blocks,
+    including the extreme scales and codes: the float64 product rounds to
+    binary32 without change."""
+    rng = np.random.default_rng(qtype)
+    nb = 64
+    blk = arc.synth_packed(qtype, 7, 1, 1, nb * 256).reshape(nb, -1).copy()
+    dpos = 0 if qtype == arc.Q4_K else 208
+    # random finite fp16 d (all exponents), including the largest ones
+    for b in range(nb):
+        bits = int(rng.integers(0x0001, 0x7BFF)) if b % 4 else 0x7BFF
+        blk[b, dpos:dpos + 2] = np.frombuffer(np.uint16(bits).tobytes(), np.uint8)
+    O = orc.oracle()
+    for b in range(nb):
+        p = blk[b].ctypes.data
+        d = np.float64(np.frombuffer(blk[b, dpos:dpos + 2].tobytes(), np.float16)[0])
+        for k in range(256):
+            if qtype == arc.Q4_K:
+                sc, mn = orc.C.c_uint32(), orc.C.c_uint32()
+                O.orc_q4k_scale_min(p, k >> 5, orc.C.byref(sc), orc.C.byref(mn))
+                prod = d * sc.value * O.orc_q4k_code(p, k)
+            else:
+                s = orc.C.c_int()
+                q = O.orc_q6k_code(p, k, orc.C.byref(s))
+                prod = d * s.value * q
+            assert np.float64(np.float32(prod)) == prod
