@@ -3,27 +3,26 @@
 // fp32 tiles).
 //
 // A prompt of M <= 256 tokens at positions pos0 .. pos0+M-1 is processed as
-// matrices: per layer
-//   RMSNorm(H) -> X (fp16)                                    k_pf_rmsnorm
-//   [q|k] = X Wqk^T  (split-K partials)                        k_pf_gemm<Q4>
-//   + bias, RoPE, q -> fp32, k -> fp16 cache rows               k_pf_qk_epi
-//   v = X Wv^T, + bias -> fp16 cache rows                       k_pf_gemm, k_pf_v_epi
+// matrices: per layer (8 launches)
+//   [q|k|v] = X [Wq|Wk|Wv]^T  (split-K partials, one launch)   k_pf_gemm_qkv
+//   + bias, RoPE on q and k, q -> fp32, k and v -> fp16 cache  k_pf_qkv_epi
 //   causal GQA over the cache (positions <= own) -> X (fp16)    k_pf_attn
-//   H += X Wo^T                                                 k_pf_gemm, k_pf_res_epi
-//   RMSNorm(H) -> X; s = silu(X Wg^T) * (X Wu^T) -> X (fp16)    k_pf_rmsnorm, k_pf_gemm<SWIGLU>
-//   H += s Wd^T                                                 k_pf_gemm, k_pf_res_epi
-// then the output RMSNorm + LM head + argmax on the last row only (the
-// decode step's kernels), leaving the argmax as the next token.
+//   H += X Wo^T, X = RMSNorm(H) (ffn norm)                      k_pf_gemm, k_pf_res_norm
+//   s = silu(X Wg^T) * (X Wu^T) -> fp16                         k_pf_gemm<SWIGLU>
+//   H += s Wd^T, X = RMSNorm(H) (next layer's attention norm)   k_pf_gemm, k_pf_res_norm
+// after the embedding and the first layer's attention norm (k_pf_embed,
+// k_pf_rmsnorm), then the output RMSNorm + LM head + argmax on the last row
+// only (the decode step's kernels), leaving the argmax as the next token.
 //
-// GEMM (k_pf_gemm): Y[m][n] = sum_k X[m][k] W[n][k] with
+// GEMM (pf_gemm_body): Y[m][n] = sum_k X[m][k] W[n][k] with
 // v_mfma_f32_32x32x16_f16.  A workgroup owns all M rows (MB blocks of 32) and
-// 128 weight rows (4 waves x 32); X is staged through LDS in half-super-block
-// tiles (double-buffered, rows padded by 8 halves so the 16-byte fragment
-// reads are bank-conflict free); each lane dequantises its own B fragment
-// (8 consecutive weights of one row per 16-wide K step) straight from the
-// packed super-block into fp16 registers: w = (d*sc)*q - dmin*mn (Q4_K) or
-// (d*sc)*q (Q6_K) in fp32, as the element decode, then rounded to fp16.
-// Operands are fp16, accumulation fp32.
+// 128*NF weight rows (4 waves, NF rows per lane); X is staged through LDS in
+// half-super-block tiles (double-buffered, rows padded by 8 halves so the
+// 16-byte fragment reads are bank-conflict free); each lane dequantises its
+// own B fragments (8 weights of one row per 16-wide K step) straight from the
+// packed super-block into fp16 registers with the element decode's fp32
+// arithmetic, software-pipelined against the MFMAs.  Operands are fp16,
+// accumulation fp32.
 #include "arc_session.hpp"
 
 #include <algorithm>
@@ -77,7 +76,9 @@ struct PfGemm {
     uint32_t mpad;       // rows of the partial buffer per split
     const _Float16* x;   // [>= MB*32 rows][ldx]
     uint32_t ldx;
-    float* out;          // PLAIN: [split][mpad][N]
+    float* out;          // PLAIN: [split][mpad][ldo], columns [0, N)
+    uint32_t ldo;
+    uint32_t tiles;      // column tiles (workgroups along x) of this operand
     _Float16* s;         // SWIGLU: [M][lds_out]
     uint32_t lds_out;
 };
@@ -394,15 +395,15 @@ __device__ __forceinline__ void pf_half(const XSrc& p, PfState<FMT, MB, NF>& s, 
 
 // Y = X W^T over super-blocks [kb0, kb1) of K for MB*32 rows of X.
 // Workgroup: 4 waves, one per SIMD; lane (l%32) of wave w owns weight row(s)
-//   SWIGLU (NF = 2): gate and up row c = blockIdx.x*128 + w*32 + l%32, and
+//   SWIGLU (NF = 2): gate and up row c = tile*128 + w*32 + l%32, and
 //                    writes s[m][c] = silu(X Wg^T)[m][c] * (X Wu^T)[m][c];
-//   PLAIN:           rows c_j = blockIdx.x*128*NF + w*32*NF + j*32 + l%32
+//   PLAIN:           rows c_j = tile*128*NF + w*32*NF + j*32 + l%32
 //                    (row c < ncol0 from w0, else row c - ncol0 of w1), and
-//                    writes split partials out[blockIdx.y][m][c].
+//                    writes split partials out[blockIdx.y][m][c] (row stride ldo).
 // X is staged in LDS half a super-block (128 K columns) at a time, double-
 // buffered; the weights of super-block kb+1 are loaded during kb.
 template <int FMT, int MB, int NF, bool SWIGLU>
-__global__ __launch_bounds__(256, 1) void k_pf_gemm(PfGemm p)
+__device__ __forceinline__ void pf_gemm_body(const PfGemm& p, uint32_t tile)
 {
     static_assert(!SWIGLU || NF == 2, "SwiGLU pairs a gate and an up row per lane");
     extern __shared__ _Float16 ash[];  // [2][MB*32][kPfLd]
@@ -416,10 +417,10 @@ __global__ __launch_bounds__(256, 1) void k_pf_gemm(PfGemm p)
 #pragma unroll
     for (int j = 0; j < NF; ++j) {
         if constexpr (SWIGLU) {
-            col[j] = blockIdx.x * 128 + wave * 32 + (lane & 31);
+            col[j] = tile * 128 + wave * 32 + (lane & 31);
             wrow[j] = (j == 0 ? p.w0 : p.w1) + uint64_t(min(col[j], p.N - 1)) * p.row_bytes;
         } else {
-            col[j] = blockIdx.x * (128 * NF) + wave * (32 * NF) + j * 32 + (lane & 31);
+            col[j] = tile * (128 * NF) + wave * (32 * NF) + j * 32 + (lane & 31);
             const uint32_t r = min(col[j], p.N - 1);
             wrow[j] = r < p.ncol0 ? p.w0 + uint64_t(r) * p.row_bytes : p.w1 + uint64_t(r - p.ncol0) * p.row_bytes;
         }
@@ -492,16 +493,34 @@ __global__ __launch_bounds__(256, 1) void k_pf_gemm(PfGemm p)
 #pragma unroll
         for (int j = 0; j < NF; ++j) {
             if (col[j] >= p.N) continue;
-            float* o = p.out + uint64_t(blockIdx.y) * p.mpad * p.N + col[j];
+            float* o = p.out + uint64_t(blockIdx.y) * p.mpad * p.ldo + col[j];
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const uint32_t m = mb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-                    if (m < p.M) o[uint64_t(m) * p.N] = s.acc[j][mb][i];
+                    if (m < p.M) o[uint64_t(m) * p.ldo] = s.acc[j][mb][i];
                 }
         }
     }
+}
+
+template <int FMT, int MB, int NF, bool SWIGLU>
+__global__ __launch_bounds__(256, 1) void k_pf_gemm(PfGemm p)
+{
+    pf_gemm_body<FMT, MB, NF, SWIGLU>(p, blockIdx.x);
+}
+
+// The q|k (Q4_K) and v (format VF) projections of one layer in one launch:
+// tiles [0, qk.tiles) are q|k, the rest v; both write split partials into
+// one [split][mpad][hidden + 2*kv_dim] buffer (v after q|k).
+template <int MB, int VF>
+__global__ __launch_bounds__(256, 1) void k_pf_gemm_qkv(PfGemm qk, PfGemm v)
+{
+    if (blockIdx.x < qk.tiles)
+        pf_gemm_body<kFmtQ4, MB, 1, false>(qk, blockIdx.x);
+    else
+        pf_gemm_body<VF, MB, 1, false>(v, blockIdx.x - qk.tiles);
 }
 
 // --------------------------------------------------------- small kernels
@@ -548,14 +567,18 @@ __global__ __launch_bounds__(256) void k_pf_rmsnorm(const float* __restrict__ h,
     for (uint32_t i = threadIdx.x; i < n; i += 256) o[i] = _Float16((r[i] * inv) * w[i]);
 }
 
-// q/k: per (m, column pair): fixed-order sum of the split partials + bias,
-// RoPE on the pair, q -> fp32, k -> fp16 cache row pos0 + m.
-__global__ __launch_bounds__(256) void k_pf_qk_epi(const float* __restrict__ part, uint32_t splits, uint32_t mpad,
-                                                   uint32_t hidden, uint32_t kv_dim, const float* __restrict__ qb,
-                                                   const float* __restrict__ kb, const float2* __restrict__ rope,
-                                                   uint32_t pos0, float* __restrict__ q, _Float16* __restrict__ kc)
+// q|k|v epilogue, per (m, column pair) of the [hidden | kv_dim | kv_dim]
+// partials: fixed-order sum over the splits + bias; q and k pairs are
+// rotated (RoPE at position pos0 + m), q -> fp32, k and v -> fp16 cache row
+// pos0 + m.
+__global__ __launch_bounds__(256) void k_pf_qkv_epi(const float* __restrict__ part, uint32_t splits, uint32_t mpad,
+                                                    uint32_t hidden, uint32_t kv_dim, const float* __restrict__ qb,
+                                                    const float* __restrict__ kb, const float* __restrict__ vb,
+                                                    const float2* __restrict__ rope, uint32_t pos0,
+                                                    float* __restrict__ q, _Float16* __restrict__ kc,
+                                                    _Float16* __restrict__ vc)
 {
-    const uint32_t N = hidden + kv_dim, m = blockIdx.y;
+    const uint32_t N = hidden + 2 * kv_dim, m = blockIdx.y;
     const uint32_t c = 2 * (blockIdx.x * 256 + threadIdx.x);
     if (c >= N) return;
     float a = 0.0f, b = 0.0f;
@@ -563,6 +586,13 @@ __global__ __launch_bounds__(256) void k_pf_qk_epi(const float* __restrict__ par
         const float2 v = *reinterpret_cast<const float2*>(part + (uint64_t(s) * mpad + m) * N + c);
         a += v.x;
         b += v.y;
+    }
+    if (c >= hidden + kv_dim) {
+        const uint32_t lc = c - hidden - kv_dim;
+        _Float16* dst = vc + uint64_t(pos0 + m) * kv_dim + lc;
+        dst[0] = _Float16(a + vb[lc]);
+        dst[1] = _Float16(b + vb[lc + 1]);
+        return;
     }
     const bool isq = c < hidden;
     const uint32_t lc = isq ? c : c - hidden;
@@ -581,27 +611,52 @@ __global__ __launch_bounds__(256) void k_pf_qk_epi(const float* __restrict__ par
     }
 }
 
-// v: fixed-order split sum + bias -> fp16 cache row pos0 + m.
-__global__ __launch_bounds__(256) void k_pf_v_epi(const float* __restrict__ part, uint32_t splits, uint32_t mpad,
-                                                  uint32_t kv_dim, const float* __restrict__ vb, uint32_t pos0,
-                                                  _Float16* __restrict__ vc)
+// H[m] += fixed-order split sum; with NORM also X[m] = fp16((H[m] * inv) *
+// w), inv = 1/sqrt(mean(H[m]^2) + eps), the next RMSNorm.  Grid M, one row
+// per workgroup of 1024 threads; thread t owns columns t + 1024*k (k < 20:
+// n <= 20480, the model limit on hidden), whose split partials are loaded
+// column-parallel ahead of the in-order sums.
+constexpr int kResCols = 20;
+template <bool NORM>
+__global__ __launch_bounds__(1024) void k_pf_res_norm(const float* __restrict__ part, uint32_t splits, uint32_t mpad,
+                                                      uint32_t n, float* __restrict__ h, const float* __restrict__ w,
+                                                      float eps, _Float16* __restrict__ x, uint32_t ldx)
 {
-    const uint32_t m = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= kv_dim) return;
-    float a = 0.0f;
-    for (uint32_t s = 0; s < splits; ++s) a += part[(uint64_t(s) * mpad + m) * kv_dim + c];
-    vc[uint64_t(pos0 + m) * kv_dim + c] = _Float16(a + vb[c]);
-}
-
-// H[m][c] += fixed-order split sum.
-__global__ __launch_bounds__(256) void k_pf_res_epi(const float* __restrict__ part, uint32_t splits, uint32_t mpad,
-                                                    uint32_t n, float* __restrict__ h)
-{
-    const uint32_t m = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= n) return;
-    float a = 0.0f;
-    for (uint32_t s = 0; s < splits; ++s) a += part[(uint64_t(s) * mpad + m) * n + c];
-    h[uint64_t(m) * n + c] = h[uint64_t(m) * n + c] + a;
+    __shared__ float red[16];
+    const uint32_t m = blockIdx.x, t = threadIdx.x;
+    float* r = h + uint64_t(m) * n;
+    const float* pm = part + uint64_t(m) * n;
+    const uint64_t sstride = uint64_t(mpad) * n;
+    float a[kResCols];
+#pragma unroll
+    for (int k = 0; k < kResCols; ++k) a[k] = 0.0f;
+    for (uint32_t s = 0; s < splits; ++s) {
+#pragma unroll
+        for (int k = 0; k < kResCols; ++k) {
+            const uint32_t c = t + 1024u * k;
+            if (c < n) a[k] += pm[s * sstride + c];
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kResCols; ++k) {
+        const uint32_t c = t + 1024u * k;
+        if (c < n) {
+            a[k] = r[c] + a[k];
+            r[c] = a[k];
+            if constexpr (NORM) ss = __builtin_fmaf(a[k], a[k], ss);
+        }
+    }
+    if constexpr (NORM) {
+        ss = block_sum<1024>(ss, red);
+        const float inv = 1.0f / sqrtf(ss / float(n) + eps);
+        _Float16* o = x + uint64_t(m) * ldx;
+#pragma unroll
+        for (int k = 0; k < kResCols; ++k) {
+            const uint32_t c = t + 1024u * k;
+            if (c < n) o[c] = _Float16((a[k] * inv) * w[c]);
+        }
+    }
 }
 
 // Causal GQA for query row m (position pos0 + m) and kv head g: the HPK q
@@ -745,6 +800,37 @@ hipError_t launch_gemm_mb(const PfGemm& p, uint32_t mb, uint32_t gx, uint32_t sp
     }
 }
 
+template <int MB, int VF>
+hipError_t launch_qkv_t(const PfGemm& qk, const PfGemm& v, uint32_t splits, hipStream_t st)
+{
+    const size_t lds = size_t(2) * MB * 32 * kPfLd * sizeof(_Float16);
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm_qkv<MB, VF>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_pf_gemm_qkv<MB, VF>), dim3(qk.tiles + v.tiles, splits), dim3(256), lds, st, qk, v);
+    return hipGetLastError();
+}
+
+template <int VF>
+hipError_t launch_qkv_mb(const PfGemm& qk, const PfGemm& v, uint32_t mb, uint32_t splits, hipStream_t st)
+{
+    switch (mb) {
+    case 1: return launch_qkv_t<1, VF>(qk, v, splits, st);
+    case 2: return launch_qkv_t<2, VF>(qk, v, splits, st);
+    case 4: return launch_qkv_t<4, VF>(qk, v, splits, st);
+    default: return launch_qkv_t<8, VF>(qk, v, splits, st);
+    }
+}
+
+hipError_t launch_qkv(const PfGemm& qk, const PfGemm& v, int vtype, uint32_t mb, uint32_t splits, hipStream_t st)
+{
+    return vtype == kFmtQ4 ? launch_qkv_mb<kFmtQ4>(qk, v, mb, splits, st) : launch_qkv_mb<kFmtQ6>(qk, v, mb, splits, st);
+}
+
 uint32_t m_blocks(uint32_t M)
 {
     const uint32_t b = (M + 31) / 32;
@@ -805,14 +891,13 @@ int ensure_bufs(arc_session* S)
     };
     const uint32_t kvd = d.kv_heads * kHeadDim;
     size_t part = 0;
-    const uint32_t shapes[3][2] = {{d.hidden + kvd, d.hidden / kQK}, {kvd, d.hidden / kQK}, {d.hidden, d.hidden / kQK}};
-    for (const auto& sh : shapes) {
+    {   // q|k|v (one launch), o, down: [split][256][columns] partials
         uint32_t gx, sp, bps;
-        split_plan(sh[0], sh[1], gx, sp, bps);
-        part = std::max(part, size_t(sp) * kPfMaxM * sh[0]);
-    }
-    {
-        uint32_t gx, sp, bps;
+        const uint32_t qkv_cols = ((d.hidden + kvd + 127) / 128 + (kvd + 127) / 128) * 128;
+        split_plan(qkv_cols, d.hidden / kQK, gx, sp, bps);
+        part = std::max(part, size_t(sp) * kPfMaxM * (d.hidden + 2 * kvd));
+        split_plan(d.hidden, d.hidden / kQK, gx, sp, bps);
+        part = std::max(part, size_t(sp) * kPfMaxM * d.hidden);
         split_plan(d.hidden, d.ffn / kQK, gx, sp, bps);
         part = std::max(part, size_t(sp) * kPfMaxM * d.hidden);
     }
@@ -884,8 +969,10 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             const Layer& L = Mdl->layers[l];
             _Float16* kc = S->kcache + uint64_t(l) * S->max_ctx * kvd;
             _Float16* vc = S->vcache + uint64_t(l) * S->max_ctx * kvd;
-            hipLaunchKernelGGL(k_pf_rmsnorm, dim3(M), dim3(256), 0, st, pf->h, H, L.attn_norm, d.rms_eps, pf->x, H);
-            if ((rc = chk(hipGetLastError(), "attn norm"))) return rc;
+            if (l == 0) {  // later layers: fused into the previous layer's down residual
+                hipLaunchKernelGGL(k_pf_rmsnorm, dim3(M), dim3(256), 0, st, pf->h, H, L.attn_norm, d.rms_eps, pf->x, H);
+                if ((rc = chk(hipGetLastError(), "attn norm"))) return rc;
+            }
 
             PfGemm g{};
             g.M = M;
@@ -895,49 +982,44 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             g.nb = H / kQK;
             g.out = pf->part;
             uint32_t gx, sp, bps;
-            // q | k
+            // q | k | v in one launch, partials [split][mpad][H | kvd | kvd]
+            const uint32_t nqkv = H + 2 * kvd;
             g.w0 = L.q;
             g.w1 = L.k;
             g.row_bytes = uint64_t(g.nb) * kQ4Bytes;
             g.ncol0 = H;
             g.N = H + kvd;
-            split_plan(g.N, g.nb, gx, sp, bps);
-            g.bps = bps;
-            if ((rc = chk(launch_gemm_mb<kFmtQ4, 1, false>(g, mb, gx, sp, st), "q/k projection"))) return rc;
-            hipLaunchKernelGGL(k_pf_qk_epi, dim3((g.N / 2 + 255) / 256, M), dim3(256), 0, st, pf->part, sp,
-                               uint32_t(kPfMaxM), H, kvd, L.qb, L.kb, S->rope, p0, pf->q, kc);
-            if ((rc = chk(hipGetLastError(), "q/k epilogue"))) return rc;
-            // v
-            g.w0 = g.w1 = L.v;
-            g.row_bytes = uint64_t(g.nb) * (L.v_type == kFmtQ4 ? kQ4Bytes : kQ6Bytes);
-            g.ncol0 = kvd;
-            g.N = kvd;
-            split_plan(g.N, g.nb, gx, sp, bps);
-            g.bps = bps;
-            rc = chk(L.v_type == kFmtQ4 ? launch_gemm_mb<kFmtQ4, 1, false>(g, mb, gx, sp, st)
-                                        : launch_gemm_mb<kFmtQ6, 1, false>(g, mb, gx, sp, st),
-                     "v projection");
-            if (rc) return rc;
-            hipLaunchKernelGGL(k_pf_v_epi, dim3((kvd + 255) / 256, M), dim3(256), 0, st, pf->part, sp,
-                               uint32_t(kPfMaxM), kvd, L.vb, p0, vc);
-            if ((rc = chk(hipGetLastError(), "v epilogue"))) return rc;
+            g.ldo = nqkv;
+            g.tiles = (g.N + 127) / 128;
+            PfGemm gv = g;
+            gv.w0 = gv.w1 = L.v;
+            gv.row_bytes = uint64_t(g.nb) * (L.v_type == kFmtQ4 ? kQ4Bytes : kQ6Bytes);
+            gv.ncol0 = kvd;
+            gv.N = kvd;
+            gv.out = pf->part + (H + kvd);
+            gv.tiles = (kvd + 127) / 128;
+            split_plan(g.tiles * 128 + gv.tiles * 128, g.nb, gx, sp, bps);
+            g.bps = gv.bps = bps;
+            if ((rc = chk(launch_qkv(g, gv, L.v_type, mb, sp, st), "q/k/v projection"))) return rc;
+            hipLaunchKernelGGL(k_pf_qkv_epi, dim3((nqkv / 2 + 255) / 256, M), dim3(256), 0, st, pf->part, sp,
+                               uint32_t(kPfMaxM), H, kvd, L.qb, L.kb, L.vb, S->rope, p0, pf->q, kc, vc);
+            if ((rc = chk(hipGetLastError(), "q/k/v epilogue"))) return rc;
             // attention -> x
             launch_attn(hpk, dim3(M, d.kv_heads), st, pf->q, kc, vc, d.kv_heads, p0, scale, pf->x, H);
             if ((rc = chk(hipGetLastError(), "prefill attention"))) return rc;
-            // o + residual
+            // o + residual + ffn norm
             g.w0 = g.w1 = L.o;
             g.row_bytes = uint64_t(g.nb) * kQ4Bytes;
             g.ncol0 = H;
             g.N = H;
+            g.ldo = H;
             split_plan(g.N, g.nb, gx, sp, bps);
             g.bps = bps;
             if ((rc = chk(launch_gemm_mb<kFmtQ4, 1, false>(g, mb, gx, sp, st), "o projection"))) return rc;
-            hipLaunchKernelGGL(k_pf_res_epi, dim3((H + 255) / 256, M), dim3(256), 0, st, pf->part, sp,
-                               uint32_t(kPfMaxM), H, pf->h);
-            if ((rc = chk(hipGetLastError(), "o residual"))) return rc;
-            // ffn norm, gate/up + SwiGLU -> xs
-            hipLaunchKernelGGL(k_pf_rmsnorm, dim3(M), dim3(256), 0, st, pf->h, H, L.ffn_norm, d.rms_eps, pf->x, H);
-            if ((rc = chk(hipGetLastError(), "ffn norm"))) return rc;
+            hipLaunchKernelGGL(k_pf_res_norm<true>, dim3(M), dim3(1024), 0, st, pf->part, sp, uint32_t(kPfMaxM), H,
+                               pf->h, L.ffn_norm, d.rms_eps, pf->x, H);
+            if ((rc = chk(hipGetLastError(), "o residual + ffn norm"))) return rc;
+            // gate/up + SwiGLU -> xs
             PfGemm u = g;
             u.w0 = L.gate;
             u.w1 = L.up;
@@ -948,7 +1030,7 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             u.s = pf->xs;
             u.lds_out = F;
             if ((rc = chk(launch_gemm_mb<kFmtQ4, 2, true>(u, mb, (F + 127) / 128, 1, st), "gate/up"))) return rc;
-            // down + residual
+            // down + residual (+ the next layer's attention norm)
             PfGemm dn = g;
             dn.x = pf->xs;
             dn.ldx = F;
@@ -957,14 +1039,20 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             dn.row_bytes = uint64_t(dn.nb) * (L.down_type == kFmtQ4 ? kQ4Bytes : kQ6Bytes);
             dn.ncol0 = H;
             dn.N = H;
+            dn.ldo = H;
             split_plan(dn.N, dn.nb, gx, sp, bps);
             dn.bps = bps;
             rc = chk(L.down_type == kFmtQ4 ? launch_gemm_mb<kFmtQ4, 1, false>(dn, mb, gx, sp, st)
                                            : launch_gemm_mb<kFmtQ6, 1, false>(dn, mb, gx, sp, st),
                      "down projection");
             if (rc) return rc;
-            hipLaunchKernelGGL(k_pf_res_epi, dim3((H + 255) / 256, M), dim3(256), 0, st, pf->part, sp,
-                               uint32_t(kPfMaxM), H, pf->h);
+            if (l + 1 < d.layers) {
+                hipLaunchKernelGGL(k_pf_res_norm<true>, dim3(M), dim3(1024), 0, st, pf->part, sp, uint32_t(kPfMaxM), H,
+                                   pf->h, Mdl->layers[l + 1].attn_norm, d.rms_eps, pf->x, H);
+            } else {
+                hipLaunchKernelGGL(k_pf_res_norm<false>, dim3(M), dim3(1024), 0, st, pf->part, sp, uint32_t(kPfMaxM),
+                                   H, pf->h, nullptr, 0.0f, nullptr, 0u);
+            }
             if ((rc = chk(hipGetLastError(), "down residual"))) return rc;
         }
         if (pass + 1 == passes) {

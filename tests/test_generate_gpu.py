@@ -78,8 +78,8 @@ def test_generate_cli_matches_oracle(tmp_path):
     assert tokens_match(gpu, ref, second, margins, scale) >= max_new // 2
     st = res["stats"]
     per_step = 3 + 7 * d.layers
-    # batched prompt pass: embed, 12 launches per layer, LM head + next token
-    assert st["prefill_dispatches"] == 1 + 12 * d.layers + 2 and st["prefill_submits"] == 1
+    # batched prompt pass: embed + first norm, 8 launches per layer, LM head + next token
+    assert st["prefill_dispatches"] == 8 * d.layers + 4 and st["prefill_submits"] == 1
     assert st["decode_dispatches_per_step"] == per_step and st["decode_submits_per_step"] == 1
     assert st["decode_steps"] == max_new - 1 and st["route_a_steps"] == max_new - 1
     assert st["route_b_steps"] == 0 and st["finite"] is True

@@ -109,7 +109,7 @@ def test_mfma_prefill_matches_oracle(n):
     rng = np.random.default_rng(n)
     prompt = rng.integers(0, d.vocab, n).astype(np.uint32)
     s, *_ = check_prompt(d, T, prompt, 512)
-    assert s.prefill_kernels == 1 + 12 * d.layers + 2
+    assert s.prefill_kernels == 8 * d.layers + 4
 
 
 def test_mfma_prefill_two_passes_and_offset():
