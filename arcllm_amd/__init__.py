@@ -21,6 +21,7 @@ LIB_PATH = os.path.join(_PKG, "libarcllm_hip.so")
 
 Q4_K = 12
 Q6_K = 14
+EXEC148 = 148  # Q4_K repacked as EXEC148 blocks (arc_gemv / arc_gemv_splitk only)
 QK = 256
 BLOCK_BYTES = {Q4_K: 144, Q6_K: 210}
 
@@ -83,6 +84,8 @@ _SIGS = {
     "arc_tune_force": [C.c_int, C.c_int],
     "arc_tune_waves": [C.c_int],
     "arc_probe_read": [_P, C.c_size_t, _P, _U32, _P],
+    "arc_exec148_materialize": [_P, _U32, _U32, _P, _P],
+    "arc_exec148_validate": [_P, _P, _U32, _U32, C.POINTER(_U64), _P],
 }
 _RESTYPE = {
     "arc_last_error": C.c_char_p,
@@ -327,6 +330,18 @@ def gemv_splitk(qtype: int, w, rows: int, K: int, splits: int, x, partials, y, r
                 stream: Optional[Stream] = None) -> None:
     check(lib().arc_gemv_splitk(qtype, _ptr(w), rows, K, splits, _ptr(x), _ptr(partials), _ptr(residual),
                                 _ptr(y), _sp(stream)))
+
+
+def exec148_materialize(q4, rows: int, K: int, exec148, stream: Optional[Stream] = None) -> None:
+    """EXEC148 image of a device Q4_K tensor into `exec148` (rows*(K/256)*148 bytes)."""
+    check(lib().arc_exec148_materialize(_ptr(q4), rows, K, _ptr(exec148), _sp(stream)))
+
+
+def exec148_validate(q4, exec148, rows: int, K: int, stream: Optional[Stream] = None) -> int:
+    """Number of EXEC148 blocks that differ from the repack of their source (0 = exact)."""
+    n = C.c_uint64(0)
+    check(lib().arc_exec148_validate(_ptr(q4), _ptr(exec148), rows, K, C.byref(n), _sp(stream)))
+    return int(n.value)
 
 
 def rmsnorm(x, w, n: int, eps: float, y, stream: Optional[Stream] = None) -> None:

@@ -34,7 +34,8 @@ ARCH = "gfx950"
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function", f"--offload-arch={ARCH}"]
 
-SOURCES = ["arc_runtime.cpp", "arc_synth.cpp", "arc_kernels.hip", "arc_probe.hip", "arc_decode.hip", "arc_prefill.hip"]
+SOURCES = ["arc_runtime.cpp", "arc_synth.cpp", "arc_kernels.hip", "arc_probe.hip", "arc_decode.hip", "arc_prefill.hip",
+           "arc_exec148.hip"]
 
 
 def hipcc() -> str:

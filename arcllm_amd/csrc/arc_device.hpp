@@ -14,6 +14,8 @@ constexpr int kQ4Bytes = 144;    // Q4_K super-block
 constexpr int kQ6Bytes = 210;    // Q6_K super-block
 constexpr int kFmtQ4 = 12;
 constexpr int kFmtQ6 = 14;
+constexpr int kFmtE148 = 148;    // EXEC148: Q4_K repacked (unpacked scales, codes in element order)
+constexpr int kE148Bytes = 148;
 
 // Defined in arc_runtime.cpp.
 int set_error(int code, const char* fmt, ...);
@@ -48,9 +50,12 @@ constexpr int kXBlk = 4 * kSlot;  // 272 floats per super-block column
 //  Q6_K: lane v owns ql chunk v of both 128-element halves; it yields
 //        quarter qa = v>>1 (low nibbles) and qa+2 (high nibbles), at
 //        l = (v&1)*16 + i.
+//  EXEC148: lane v owns elements 64v .. 64v+63 (codes in element order),
+//        group t = elements 64v + 16t .. +15.
 template <int FMT>
 __device__ __host__ constexpr int x_group_offset(int v, int t)
 {
+    if (FMT == kFmtE148) return v * 64 + t * 16;
     if (FMT == kFmtQ4) {
         const int c = v + 4 * (t >> 1);
         return (c >> 1) * 64 + (t & 1) * 32 + (c & 1) * 16;

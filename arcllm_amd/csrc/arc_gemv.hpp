@@ -124,8 +124,41 @@ __device__ __forceinline__ void q6_load(const uint8_t* blk, int v, Q6Blk& o)
     o.d = t & 0xffffu;
 }
 
+// EXEC148 block (148 bytes, 4-byte aligned): bytes 0..3 d, dmin; 4 + 2j,
+// 5 + 2j the unpacked (sc_j, mn_j); from 20 the codes, element k in byte
+// 20 + k/2 (low nibble for even k).  Lane v reads the d/dmin dword, the dword
+// of its two sub-blocks' (sc, mn) and the 32 code bytes of its 64 elements;
+// every read lies inside the block.
+struct E148Blk {
+    uint32_t dm;    // d | dmin << 16
+    uint32_t sc;    // sc_{2v}, mn_{2v}, sc_{2v+1}, mn_{2v+1}
+    uint32_t c[8];  // elements 64v + 8i .. +7 in dword i
+};
+
+__device__ __forceinline__ void e148_load(const uint8_t* blk, int v, E148Blk& o)
+{
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(blk);
+    o.dm = w[0];
+    o.sc = w[1 + v];
+    const u32x4a4 a = *reinterpret_cast<const u32x4a4*>(blk + 20 + 32 * v);
+    const u32x4a4 b = *reinterpret_cast<const u32x4a4*>(blk + 36 + 32 * v);
+    o.c[0] = a.x;
+    o.c[1] = a.y;
+    o.c[2] = a.z;
+    o.c[3] = a.w;
+    o.c[4] = b.x;
+    o.c[5] = b.y;
+    o.c[6] = b.z;
+    o.c[7] = b.w;
+}
+
 template <int FMT>
 struct BlkOf;
+template <>
+struct BlkOf<kFmtE148> {
+    using T = E148Blk;
+    static constexpr int bytes = kE148Bytes;
+};
 template <>
 struct BlkOf<kFmtQ4> {
     using T = Q4Blk;
@@ -291,12 +324,82 @@ __device__ __forceinline__ void q6_dot(const Q6Blk (&b)[N], const float* xs, int
     }
 }
 
+// EXEC148: each code dword holds 8 consecutive elements, two per byte; the
+// even elements are read as fp16 subnormals q*2^-24 (w & 0x000f000f and the
+// same of w >> 8), the odd ones as q*2^-20 (w & 0x00f000f0, ...): the staged
+// x carries 2^24 on even and 2^20 on odd elements.  Groups 0, 1 belong to
+// sub-block 2v, groups 2, 3 to 2v+1:
+//   sum_k (d sc q - dmin mn) x = d sum_g sc_g (q.x)_g - dmin sum_g mn_g (sum x)_g
+template <int N>
+__device__ __forceinline__ void e148_dot(const E148Blk (&b)[N], const float* xs, float (&acc)[N])
+{
+    float a[N][4];
+#pragma unroll
+    for (int n = 0; n < N; ++n) a[n][0] = a[n][1] = a[n][2] = a[n][3] = 0.0f;
+#pragma unroll
+    for (int dw = 0; dw < 2; ++dw) {
+        float4 xl[4], xh[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            xl[t] = lds4(xs + t * 16 + dw * 8);
+            xh[t] = lds4(xs + t * 16 + dw * 8 + 4);
+        }
+#pragma unroll
+        for (int n = 0; n < N; ++n) {
+            uint32_t L[4], H[4], Lo[4], Ho[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t w = b[n].c[2 * t + dw], w8 = w >> 8;
+                L[t] = opaque(w & 0x000f000fu);
+                H[t] = opaque(w & 0x00f000f0u);
+                Lo[t] = opaque(w8 & 0x000f000fu);
+                Ho[t] = opaque(w8 & 0x00f000f0u);
+            }
+            // the four group chains advance in turn
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[n][t] = fmix(L[t], false, xl[t].x, a[n][t]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[n][t] = fmix(H[t], false, xl[t].y, a[n][t]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[n][t] = fmix(Lo[t], false, xl[t].z, a[n][t]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[n][t] = fmix(Ho[t], false, xl[t].w, a[n][t]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[n][t] = fmix(L[t], true, xh[t].x, a[n][t]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[n][t] = fmix(H[t], true, xh[t].y, a[n][t]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[n][t] = fmix(Lo[t], true, xh[t].z, a[n][t]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[n][t] = fmix(Ho[t], true, xh[t].w, a[n][t]);
+        }
+    }
+    const float4 S = lds4(xs + 64);
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+        const float sc0 = byte_f(b[n].sc, 0), mn0 = byte_f(b[n].sc, 1);
+        const float sc1 = byte_f(b[n].sc, 2), mn1 = byte_f(b[n].sc, 3);
+        float qs = sc0 * a[n][0];
+        qs = __builtin_fmaf(sc0, a[n][1], qs);
+        qs = __builtin_fmaf(sc1, a[n][2], qs);
+        qs = __builtin_fmaf(sc1, a[n][3], qs);
+        float ms = mn0 * S.x;
+        ms = __builtin_fmaf(mn0, S.y, ms);
+        ms = __builtin_fmaf(mn1, S.z, ms);
+        ms = __builtin_fmaf(mn1, S.w, ms);
+        acc[n] = fmix(b[n].dm, false, qs, acc[n]);   // + d * qs
+        acc[n] = fmix(b[n].dm, true, -ms, acc[n]);   // - dmin * ms
+    }
+}
+
 template <int FMT, int N>
 __device__ __forceinline__ void blk_dot(const typename BlkOf<FMT>::T (&b)[N], const float* xs, int v,
                                         float (&acc)[N])
 {
     if constexpr (FMT == kFmtQ4)
         q4_dot<N>(b, xs, v, acc);
+    else if constexpr (FMT == kFmtE148)
+        e148_dot<N>(b, xs, acc);
     else
         q6_dot<N>(b, xs, v, acc);
 }
@@ -306,6 +409,8 @@ __device__ __forceinline__ void blk_load(const uint8_t* blk, int v, typename Blk
 {
     if constexpr (FMT == kFmtQ4)
         q4_load(blk, v, o);
+    else if constexpr (FMT == kFmtE148)
+        e148_load(blk, v, o);
     else
         q6_load(blk, v, o);
 }
@@ -334,6 +439,8 @@ __device__ __forceinline__ void put_group(float* lds, uint32_t gi, const float4 
     const uint32_t bl = gi >> 4, v = (gi >> 2) & 3u, t = gi & 3u;
     float* dst = lds + bl * kXBlk + v * kSlot + t * 16;
     const float unit = (FMT == kFmtQ4 && (t & 1u)) ? 1048576.0f : 16777216.0f;  // 2^20 : 2^24
+    // EXEC148: 2^24 on even elements, 2^20 on odd ones
+    const float uo = FMT == kFmtE148 ? 1048576.0f : unit;
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -341,7 +448,7 @@ __device__ __forceinline__ void put_group(float* lds, uint32_t gi, const float4 
         s += q[i].y;
         s += q[i].z;
         s += q[i].w;
-        reinterpret_cast<float4*>(dst)[i] = make_float4(q[i].x * unit, q[i].y * unit, q[i].z * unit, q[i].w * unit);
+        reinterpret_cast<float4*>(dst)[i] = make_float4(q[i].x * unit, q[i].y * uo, q[i].z * unit, q[i].w * uo);
     }
     lds[bl * kXBlk + v * kSlot + 64 + t] = s;
 }
@@ -845,6 +952,12 @@ template <int EPI>
 hipError_t launch_gemv(int qtype, const Cfg& c, const GemvParams& p, uint32_t splits, hipStream_t s, uint32_t* gx)
 {
     if (qtype == kFmtQ4) return launch_cfg<kFmtQ4, EPI>(c, p, splits, s, gx);
+    if (qtype == kFmtE148) {
+        // EXEC148 is the down projection's representation: plain and split-K only
+        if constexpr (EPI == EPI_PLAIN || EPI == EPI_PARTIAL || EPI == EPI_COLPART)
+            return launch_cfg<kFmtE148, EPI>(c, p, splits, s, gx);
+        return hipErrorInvalidValue;
+    }
     return launch_cfg<kFmtQ6, EPI>(c, p, splits, s, gx);
 }
 
@@ -860,11 +973,12 @@ inline hipError_t launch_gemv_epi(int epi, int qtype, const Cfg& c, const GemvPa
     }
 }
 
-static int block_bytes(int qtype) { return qtype == kFmtQ4 ? kQ4Bytes : kQ6Bytes; }
+static int block_bytes(int qtype) { return qtype == kFmtQ4 ? kQ4Bytes : qtype == kFmtE148 ? kE148Bytes : kQ6Bytes; }
 
 static int check_shape(int qtype, const void* w, uint32_t rows, uint32_t K)
 {
-    if (qtype != kFmtQ4 && qtype != kFmtQ6) return set_error(ARC_ERR_UNSUPPORTED, "unsupported qtype %d", qtype);
+    if (qtype != kFmtQ4 && qtype != kFmtQ6 && qtype != kFmtE148)
+        return set_error(ARC_ERR_UNSUPPORTED, "unsupported qtype %d", qtype);
     if (!w) return set_error(ARC_ERR_INVALID_ARGUMENT, "null weight pointer");
     if (rows == 0 || K == 0 || (K % kQK) != 0)
         return set_error(ARC_ERR_INVALID_ARGUMENT, "bad shape rows=%u K=%u (K must be a nonzero multiple of 256)",
@@ -872,6 +986,7 @@ static int check_shape(int qtype, const void* w, uint32_t rows, uint32_t K)
     const uintptr_t a = reinterpret_cast<uintptr_t>(w);
     if (qtype == kFmtQ4 && (a & 15u)) return set_error(ARC_ERR_INVALID_ARGUMENT, "Q4_K tensor not 16-byte aligned");
     if (qtype == kFmtQ6 && (a & 1u)) return set_error(ARC_ERR_INVALID_ARGUMENT, "Q6_K tensor not 2-byte aligned");
+    if (qtype == kFmtE148 && (a & 3u)) return set_error(ARC_ERR_INVALID_ARGUMENT, "EXEC148 tensor not 4-byte aligned");
     return ARC_OK;
 }
 

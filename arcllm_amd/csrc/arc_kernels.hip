@@ -161,6 +161,7 @@ int arc_tune_waves(int waves)
 
 int arc_dequant(int qtype, const void* w, uint32_t rows, uint32_t K, float* out, arc_stream_t stream)
 {
+    if (qtype == kFmtE148) return set_error(ARC_ERR_UNSUPPORTED, "arc_dequant takes Q4_K or Q6_K");
     int rc = check_shape(qtype, w, rows, K);
     if (rc) return rc;
     if (!out) return set_error(ARC_ERR_INVALID_ARGUMENT, "null output");
@@ -191,6 +192,7 @@ int arc_gemv(int qtype, const void* w, uint32_t rows, uint32_t K, const float* x
 int arc_gateup_swiglu(int qtype, const void* w_gate, const void* w_up, uint32_t rows, uint32_t K, const float* x,
                       float* s, arc_stream_t stream)
 {
+    if (qtype == kFmtE148) return set_error(ARC_ERR_UNSUPPORTED, "fused gate/up takes Q4_K or Q6_K");
     int rc = check_shape(qtype, w_gate, rows, K);
     if (rc) return rc;
     if ((rc = check_shape(qtype, w_up, rows, K))) return rc;
@@ -257,6 +259,7 @@ size_t arc_lmhead_workspace_bytes(int qtype, uint32_t rows, uint32_t K)
 int arc_lmhead_argmax(int qtype, const void* w, uint32_t rows, uint32_t K, const float* h, const float* normw,
                       float eps, float* logits, void* workspace, uint32_t* out, arc_stream_t stream)
 {
+    if (qtype == kFmtE148) return set_error(ARC_ERR_UNSUPPORTED, "the LM head takes Q4_K or Q6_K");
     int rc = check_shape(qtype, w, rows, K);
     if (rc) return rc;
     if ((rc = check_vec(h, "h"))) return rc;

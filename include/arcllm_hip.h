@@ -46,8 +46,10 @@ typedef enum arc_status {
 } arc_status;
 
 typedef enum arc_qtype {
-    ARC_Q4_K = 12, /* ggml type id of Q4_K (src/arcllm_v1_runtime.cpp:168) */
-    ARC_Q6_K = 14  /* ggml type id of Q6_K */
+    ARC_Q4_K = 12,     /* ggml type id of Q4_K (src/arcllm_v1_runtime.cpp:168) */
+    ARC_Q6_K = 14,     /* ggml type id of Q6_K */
+    ARC_EXEC148 = 148  /* Q4_K repacked as EXEC148 (src/q4_down_exec148_materializer.h:14-17):
+                          accepted by arc_gemv and arc_gemv_splitk */
 } arc_qtype;
 
 typedef void *arc_stream_t; /* a hipStream_t; NULL is the default stream */
@@ -112,6 +114,23 @@ int arc_gateup_swiglu(int qtype, const void *w_gate, const void *w_up, uint32_t 
 int arc_gemv_splitk(int qtype, const void *w, uint32_t rows, uint32_t K, uint32_t splits,
                     const float *x, float *partials, const float *residual, float *y,
                     arc_stream_t stream);
+
+/* ---------------------------------------------------------------- EXEC148 */
+/* EXEC148 image of a Q4_K tensor (rows x K, device pointers, both 16-byte
+ * aligned): rows*(K/256) blocks of 148 bytes, d and dmin bytes, the eight
+ * unpacked (sc, mn) byte pairs, then the 256 codes two per byte in element
+ * order.  Replaces the P1 acquisition path of the Q4-down backend
+ * (shaders/b1_2_exec148_gpu_materialize.comp,
+ * src/arcllm_v1_q4_vulkan_backend_v4_runtime.h:120-141, 218-224) and
+ * materialize_tensor (src/q4_down_exec148_materializer.h:17). */
+int arc_exec148_materialize(const void *q4, uint32_t rows, uint32_t K, void *exec, arc_stream_t stream);
+
+/* *mismatched = number of EXEC148 blocks whose canonical tuple (d, dmin,
+ * (sc, mn) x 8, 256 codes) differs from their Q4_K source block's: 0 means
+ * the image is exact.  The per-block check of validate_tensor
+ * (src/q4_down_exec148_materializer.h:21-22); synchronous on `stream`. */
+int arc_exec148_validate(const void *q4, const void *exec, uint32_t rows, uint32_t K, uint64_t *mismatched,
+                         arc_stream_t stream);
 
 /* ------------------------------------------------------- norm / LM head */
 /* y = x * rsqrt(mean(x^2) + eps) * w over n elements (shaders/p7_rmsnorm_seq.comp). */

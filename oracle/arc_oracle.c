@@ -136,6 +136,151 @@ float orc_q6k_weight(const uint8_t *blk, uint32_t k)
     return a * (float)q;
 }
 
+/* ---- EXEC148: the Q4_K down-projection's route-B representation ----
+ * src/q4_down_exec148_materializer.h:14-17 (materialize_block),
+ * shaders/b1_2_exec148_gpu_materialize.comp:44-75.  A 148-byte block holds
+ * the Q4_K block's d and dmin bytes verbatim (0..3), the eight unpacked 6-bit
+ * (sc, mn) pairs as bytes 4 + 2j, 5 + 2j, and the 256 codes in element order,
+ * two per byte from byte 20: element k in byte 20 + k/2, low nibble for even
+ * k. */
+void orc_exec148_block(const uint8_t *q4, uint8_t *e)
+{
+    memcpy(e, q4, 4);
+    for (uint32_t j = 0; j < 8u; ++j) {
+        uint32_t sc, mn;
+        orc_q4k_scale_min(q4, j, &sc, &mn);
+        e[4u + 2u * j] = (uint8_t)sc;
+        e[5u + 2u * j] = (uint8_t)mn;
+    }
+    for (uint32_t p = 0; p < 128u; ++p)
+        e[20u + p] = (uint8_t)(orc_q4k_code(q4, 2u * p) | (orc_q4k_code(q4, 2u * p + 1u) << 4));
+}
+
+int orc_exec148_tensor(const uint8_t *q4, uint32_t rows, uint32_t K, uint8_t *e)
+{
+    if (K == 0u || (K % ORC_QK) != 0u) return -1;
+    const size_t nb = (size_t)rows * (K / ORC_QK);
+    for (size_t b = 0; b < nb; ++b) orc_exec148_block(q4 + b * ORC_Q4K_BLOCK_BYTES, e + b * ORC_EXEC148_BLOCK_BYTES);
+    return 0;
+}
+
+/* The validator's canonical 276-byte tuple (d, dmin bytes; (sc, mn) x 8;
+ * 256 codes) of a Q4_K block and of an EXEC148 block
+ * (src/q4_down_exec148_materializer.h:18-19, validator_source_tuple /
+ * validator_exec_tuple); a correct EXEC148 block has the same tuple as its
+ * source. */
+void orc_q4k_canon(const uint8_t *q4, uint8_t *t)
+{
+    memcpy(t, q4, 4);
+    for (uint32_t j = 0; j < 8u; ++j) {
+        uint32_t sc, mn;
+        orc_q4k_scale_min(q4, j, &sc, &mn);
+        t[4u + 2u * j] = (uint8_t)sc;
+        t[5u + 2u * j] = (uint8_t)mn;
+    }
+    for (uint32_t k = 0; k < 256u; ++k) t[20u + k] = (uint8_t)orc_q4k_code(q4, k);
+}
+
+void orc_exec148_canon(const uint8_t *e, uint8_t *t)
+{
+    memcpy(t, e, 20);
+    for (uint32_t k = 0; k < 256u; ++k) {
+        const uint8_t b = e[20u + (k >> 1)];
+        t[20u + k] = (uint8_t)((k & 1u) ? (b >> 4) : (b & 15u));
+    }
+}
+
+/* Element k of an EXEC148 block: d*sc*q - dmin*mn, the Q4_K element formula
+ * on the unpacked fields (shaders/q4_down_exec148_serial.comp). */
+float orc_exec148_weight(const uint8_t *e, uint32_t k)
+{
+    const float d = orc_half_to_float(ld16(e));
+    const float dmin = orc_half_to_float(ld16(e + 2));
+    const uint32_t j = k >> 5;
+    const uint8_t b = e[20u + (k >> 1)];
+    const uint32_t q = (k & 1u) ? (uint32_t)(b >> 4) : (uint32_t)(b & 15u);
+    const float a = d * (float)e[4u + 2u * j];
+    const float bq = a * (float)q;
+    const float c = dmin * (float)e[5u + 2u * j];
+    return bq - c;
+}
+
+/* ---- SHA-256 (FIPS 180-4) ----
+ * The round constants and initial hash are the first 32 fractional bits of
+ * the cube roots of the first 64 primes and of the square roots of the first
+ * 8 primes; they are computed here with exact integer roots. */
+static uint64_t iroot_u128(unsigned __int128 n, int cube)
+{
+    uint64_t x = (uint64_t)(cube ? cbrtl((long double)n) : sqrtl((long double)n));
+#define POW(v) (cube ? (unsigned __int128)(v) * (v) * (v) : (unsigned __int128)(v) * (v))
+    while (x > 0 && POW(x) > n) --x;
+    while (POW(x + 1) <= n) ++x;
+#undef POW
+    return x;
+}
+
+static void sha256_constants(uint32_t k[64], uint32_t h0[8])
+{
+    uint32_t primes[64], n = 0;
+    for (uint32_t c = 2; n < 64u; ++c) {
+        int is_p = 1;
+        for (uint32_t i = 0; i < n && primes[i] * primes[i] <= c; ++i)
+            if (c % primes[i] == 0u) { is_p = 0; break; }
+        if (is_p) primes[n++] = c;
+    }
+    for (uint32_t i = 0; i < 64u; ++i) k[i] = (uint32_t)iroot_u128((unsigned __int128)primes[i] << 96, 1);
+    for (uint32_t i = 0; i < 8u; ++i) h0[i] = (uint32_t)iroot_u128((unsigned __int128)primes[i] << 64, 0);
+}
+
+static uint32_t ror32(uint32_t x, uint32_t r) { return (x >> r) | (x << (32u - r)); }
+
+static void sha256_block(uint32_t st[8], const uint32_t k[64], const uint8_t *blk)
+{
+    uint32_t w[64];
+    for (uint32_t i = 0; i < 16u; ++i)
+        w[i] = ((uint32_t)blk[4 * i] << 24) | ((uint32_t)blk[4 * i + 1] << 16) | ((uint32_t)blk[4 * i + 2] << 8) |
+               (uint32_t)blk[4 * i + 3];
+    for (uint32_t i = 16; i < 64u; ++i) {
+        const uint32_t s0 = ror32(w[i - 15], 7) ^ ror32(w[i - 15], 18) ^ (w[i - 15] >> 3);
+        const uint32_t s1 = ror32(w[i - 2], 17) ^ ror32(w[i - 2], 19) ^ (w[i - 2] >> 10);
+        w[i] = w[i - 16] + s0 + w[i - 7] + s1;
+    }
+    uint32_t v[8];
+    memcpy(v, st, sizeof(v));
+    for (uint32_t i = 0; i < 64u; ++i) {
+        const uint32_t e = v[4], a = v[0];
+        const uint32_t t1 = v[7] + (ror32(e, 6) ^ ror32(e, 11) ^ ror32(e, 25)) + ((e & v[5]) ^ (~e & v[6])) + k[i] + w[i];
+        const uint32_t t2 = (ror32(a, 2) ^ ror32(a, 13) ^ ror32(a, 22)) + ((a & v[1]) ^ (a & v[2]) ^ (v[1] & v[2]));
+        memmove(v + 1, v, 7 * sizeof(uint32_t));
+        v[4] += t1;
+        v[0] = t1 + t2;
+    }
+    for (uint32_t i = 0; i < 8u; ++i) st[i] += v[i];
+}
+
+void orc_sha256(const uint8_t *p, size_t n, uint8_t out[32])
+{
+    uint32_t k[64], st[8];
+    sha256_constants(k, st);
+    size_t i = 0;
+    for (; i + 64 <= n; i += 64) sha256_block(st, k, p + i);
+    uint8_t tail[128];
+    const size_t r = n - i, tl = r < 56 ? 64 : 128;
+    memset(tail, 0, sizeof(tail));
+    if (r) memcpy(tail, p + i, r);
+    tail[r] = 0x80;
+    const uint64_t bits = (uint64_t)n * 8u;
+    for (int b = 0; b < 8; ++b) tail[tl - 1 - b] = (uint8_t)(bits >> (8 * b));
+    sha256_block(st, k, tail);
+    if (tl == 128) sha256_block(st, k, tail + 64);
+    for (uint32_t j = 0; j < 8u; ++j) {
+        out[4 * j] = (uint8_t)(st[j] >> 24);
+        out[4 * j + 1] = (uint8_t)(st[j] >> 16);
+        out[4 * j + 2] = (uint8_t)(st[j] >> 8);
+        out[4 * j + 3] = (uint8_t)st[j];
+    }
+}
+
 static int row_bytes(int qtype, uint32_t K, size_t *rb, size_t *bb)
 {
     if (K == 0u || (K % ORC_QK) != 0u) return -1;

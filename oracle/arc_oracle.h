@@ -21,7 +21,7 @@ extern "C" {
 #endif
 
 enum { ORC_Q4_K = 12, ORC_Q6_K = 14 };
-enum { ORC_Q4K_BLOCK_BYTES = 144, ORC_Q6K_BLOCK_BYTES = 210, ORC_QK = 256 };
+enum { ORC_Q4K_BLOCK_BYTES = 144, ORC_Q6K_BLOCK_BYTES = 210, ORC_EXEC148_BLOCK_BYTES = 148, ORC_QK = 256 };
 
 /* ---- element decode (bit-exact fp32) ---- */
 float orc_half_to_float(uint16_t h);
@@ -32,6 +32,14 @@ int orc_q6k_code(const uint8_t *blk, uint32_t k, int *scale);
 float orc_q6k_weight(const uint8_t *blk, uint32_t k);
 /* Dequantise rows x K (K a multiple of 256) of a packed row-major tensor. */
 int orc_dequant(int qtype, const uint8_t *w, uint32_t rows, uint32_t K, float *out);
+
+/* ---- EXEC148 (Q4_K route-B representation) ---- */
+void orc_exec148_block(const uint8_t *q4, uint8_t *e);
+int orc_exec148_tensor(const uint8_t *q4, uint32_t rows, uint32_t K, uint8_t *e);
+void orc_q4k_canon(const uint8_t *q4, uint8_t *t);        /* 276-byte canonical tuple */
+void orc_exec148_canon(const uint8_t *e, uint8_t *t);
+float orc_exec148_weight(const uint8_t *e, uint32_t k);
+void orc_sha256(const uint8_t *p, size_t n, uint8_t out[32]);
 
 /* ---- GEMV ---- */
 /* R0: serial fp32 per row, per-element decode, sum starts at bias[r] (or 0). */

@@ -57,6 +57,12 @@ def oracle() -> C.CDLL:
             "orc_q6k_code": ([_P, _U32, C.POINTER(C.c_int)], C.c_int),
             "orc_q4k_scale_min": ([_P, _U32, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)], None),
             "orc_dequant": ([C.c_int, _P, _U32, _U32, _P], C.c_int),
+            "orc_exec148_block": ([_P, _P], None),
+            "orc_exec148_tensor": ([_P, _U32, _U32, _P], C.c_int),
+            "orc_q4k_canon": ([_P, _P], None),
+            "orc_exec148_canon": ([_P, _P], None),
+            "orc_exec148_weight": ([_P, _U32], C.c_float),
+            "orc_sha256": ([_P, C.c_size_t, _P], None),
             "orc_gemv_r0": ([C.c_int, _P, _U32, _U32, _P, _P, _P], C.c_int),
             "orc_gemv_r0_mt": ([C.c_int, _P, _U32, _U32, _P, _P, _P, C.c_int], C.c_int),
             "orc_gemv_r64": ([C.c_int, _P, _U32, _U32, _P, _P, _P], C.c_int),
@@ -116,6 +122,25 @@ def dequant(qtype: int, w: np.ndarray, rows: int, K: int) -> np.ndarray:
     out = np.empty(rows * K, dtype=np.float32)
     assert oracle().orc_dequant(qtype, _p(w), rows, K, _p(out)) == 0
     return out.reshape(rows, K)
+
+
+def exec148(w: np.ndarray, rows: int, K: int) -> np.ndarray:
+    """EXEC148 image (148-byte blocks) of a packed Q4_K tensor."""
+    out = np.empty(rows * (K // 256) * 148, dtype=np.uint8)
+    assert oracle().orc_exec148_tensor(_p(w), rows, K, _p(out)) == 0
+    return out
+
+
+def sha256(data: np.ndarray) -> str:
+    buf = np.ascontiguousarray(data, dtype=np.uint8).ravel()
+    if buf.size == 0:
+        buf = np.zeros(1, np.uint8)
+        n = 0
+    else:
+        n = buf.size
+    o = np.zeros(32, np.uint8)
+    oracle().orc_sha256(_p(buf), n, _p(o))
+    return bytes(o).hex()
 
 
 def gemv_r64(qtype: int, w: np.ndarray, rows: int, K: int, x: np.ndarray, bias=None) -> np.ndarray:

@@ -245,6 +245,60 @@ def test_exec148_layout_against_oracle_decode():
             assert q == O.orc_q4k_code(_p(blk), k)
 
 
+def test_exec148_oracle_matches_reference_materializer():
+    """orc_exec148_block against the blocks the reference's own materializer
+    (src/q4_down_exec148_materializer.h) wrote into the golden file, and both
+    canonical tuples against the reference validator's source tuples."""
+    g = np.load(os.path.join(GOLD, "q4_tuples.npz"))
+    e = np.zeros(148, np.uint8)
+    t1, t2 = np.zeros(276, np.uint8), np.zeros(276, np.uint8)
+    for blk, ref_e, ref_t in zip(g["blocks"], g["exec148"], g["tuples"]):
+        blk = np.ascontiguousarray(blk)
+        O.orc_exec148_block(_p(blk), _p(e))
+        assert np.array_equal(e, ref_e)
+        O.orc_q4k_canon(_p(blk), _p(t1))
+        O.orc_exec148_canon(_p(e), _p(t2))
+        assert np.array_equal(t1, ref_t) and np.array_equal(t2, ref_t)
+        # route-B element values equal the Q4_K element decode bit for bit
+        for k in range(0, 256, 7):
+            a = np.float32(O.orc_exec148_weight(_p(e), k))
+            b = np.float32(O.orc_q4k_weight(_p(blk), k))
+            assert a.view(np.uint32) == b.view(np.uint32) or (np.isnan(a) and np.isnan(b))
+
+
+def test_exec148_tuple_mismatch_is_detected():
+    """A flipped nibble or scale byte in an EXEC148 block changes its canonical
+    tuple (what validation compares)."""
+    g = np.load(os.path.join(GOLD, "q4_tuples.npz"))
+    blk = np.ascontiguousarray(g["blocks"][3])
+    e = np.zeros(148, np.uint8)
+    O.orc_exec148_block(_p(blk), _p(e))
+    t0, t1 = np.zeros(276, np.uint8), np.zeros(276, np.uint8)
+    O.orc_q4k_canon(_p(blk), _p(t0))
+    for pos, mask in ((4, 1), (19, 32), (20, 1), (147, 0x10)):
+        bad = e.copy()
+        bad[pos] ^= mask
+        O.orc_exec148_canon(_p(bad), _p(t1))
+        assert not np.array_equal(t0, t1)
+
+
+def test_sha256_oracle_known_answers_and_hashlib():
+    """orc_sha256 against the reference's Sha256 outputs (golden KATs) and
+    against hashlib on every length 0..200 (all padding cases)."""
+    import hashlib
+    kat = json.load(open(os.path.join(GOLD, "sha256_kat.json")))
+    assert orc.sha256(np.frombuffer(b"abc", np.uint8)) == kat["abc"]
+    assert orc.sha256(np.zeros(0, np.uint8)) == kat["empty"]
+    ex = np.load(os.path.join(GOLD, "q4_tuples.npz"))["exec148"]
+    assert orc.sha256(ex[:8]) == kat["exec148_2rows"]
+    rng = np.random.default_rng(5)
+    for n in range(0, 201):
+        b = rng.integers(0, 256, n, dtype=np.uint8)
+        assert orc.sha256(b) == hashlib.sha256(bytes(b)).hexdigest(), n
+    big = rng.integers(0, 256, 1 << 16, dtype=np.uint8)
+    assert orc.sha256(big) == hashlib.sha256(bytes(big)).hexdigest()
+
+
 # ------------------------------------------------------------------ GEMV
 def _synthetic(qtype, rows, K, seed):
     rng = np.random.default_rng(seed)
