@@ -26,7 +26,8 @@ LIB = os.path.join(PKG, "libarcllm_hip.so")
 HOST = os.path.join(PKG, "host")
 RUNTIME_LIB = os.path.join(PKG, "libarcllm_runtime.so")
 CLI = os.path.join(PKG, "arcllm_runtime")
-HOST_SOURCES = ["gguf.cpp", "runtime.cpp", "inspect.cpp"]
+HOST_SOURCES = ["gguf.cpp", "runtime.cpp", "inspect.cpp", "registry_v2.cpp", "policy_v4.cpp", "binding_v4.cpp",
+                "q4_down_backend.cpp", "registrations/arcllm_v1_q4k_down_reference_registration_v2.cpp"]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 ARCH = "gfx950"
 

@@ -463,11 +463,13 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         if ((rc = chk(launch_gemv_epi(EPI_SWIGLU, kFmtQ4, choose_cfg(EPI_SWIGLU, F, H / kQK, 1), p, 1, st), "gate/up")))
             return rc;
 
-        // down + residual: h = h1 + Wd s
-        p = make_params(L.down_type, L.down, nullptr, H, F, S->s);
+        // down + residual: h = h1 + Wd s (route B: the layer's EXEC148 image)
+        const uint8_t* e148 = l < S->down_e148.size() ? S->down_e148[l] : nullptr;
+        const int dfmt = e148 ? int(kFmtE148) : L.down_type;
+        p = make_params(dfmt, e148 ? e148 : L.down, nullptr, H, F, S->s);
         p.res = S->h1;
         p.y = S->h;
-        if ((rc = chk(launch_gemv_epi(EPI_PLAIN, L.down_type, choose_cfg(EPI_PLAIN, H, F / kQK, 1), p, 1, st),
+        if ((rc = chk(launch_gemv_epi(EPI_PLAIN, dfmt, choose_cfg(EPI_PLAIN, H, F / kQK, 1), p, 1, st),
                       "down projection")))
             return rc;
     }
@@ -900,6 +902,49 @@ int arc_session_logits(arc_session* s, float* host_logits)
 }
 
 uint32_t arc_session_kernels_per_step(const arc_session* s) { return s ? s->kernels_per_step : 0; }
+
+int arc_model_tensor_device(const arc_model* model, int layer, int which, const void** ptr)
+{
+    if (!model || !ptr) return set_error(ARC_ERR_INVALID_ARGUMENT, "null argument");
+    *ptr = nullptr;
+    if (layer < 0) {
+        switch (which) {
+        case ARC_T_TOKEN_EMBD: *ptr = model->emb; break;
+        case ARC_T_OUTPUT: *ptr = model->out; break;
+        case ARC_T_OUTPUT_NORM: *ptr = model->out_norm; break;
+        default: return set_error(ARC_ERR_INVALID_ARGUMENT, "bad global tensor %d", which);
+        }
+        return ARC_OK;
+    }
+    if (uint32_t(layer) >= model->layers.size()) return set_error(ARC_ERR_INVALID_ARGUMENT, "layer %d out of range", layer);
+    if (which < 0 || which >= ARC_T_LAYER_COUNT) return set_error(ARC_ERR_INVALID_ARGUMENT, "bad layer tensor %d", which);
+    const arc::Layer& L = model->layers[layer];
+    const void* const t[ARC_T_LAYER_COUNT] = {L.attn_norm, L.q, L.k, L.v, L.qb, L.kb, L.vb, L.o, L.ffn_norm, L.gate,
+                                              L.up, L.down};
+    *ptr = t[which];
+    return ARC_OK;
+}
+
+int arc_session_route_down(arc_session* s, uint32_t layer, const void* exec148)
+{
+    if (!s) return set_error(ARC_ERR_INVALID_ARGUMENT, "null session");
+    const arc_model* m = s->model;
+    if (layer >= m->layers.size()) return set_error(ARC_ERR_INVALID_ARGUMENT, "layer %u out of range", layer);
+    if (exec148 && m->layers[layer].down_type != kFmtQ4)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "layer %u: ffn_down is not Q4_K (no EXEC148 route)", layer);
+    if (reinterpret_cast<uintptr_t>(exec148) & 15u)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "EXEC148 image not 16-byte aligned");
+    if (s->down_e148.size() != m->layers.size()) s->down_e148.assign(m->layers.size(), nullptr);
+    const uint8_t* e = static_cast<const uint8_t*>(exec148);
+    if (s->down_e148[layer] == e) return ARC_OK;
+    s->down_e148[layer] = e;
+    // the captured step reads the old route: capture again on next use
+    if (s->exec) (void)hipGraphExecDestroy(s->exec);
+    if (s->graph) (void)hipGraphDestroy(s->graph);
+    s->exec = nullptr;
+    s->graph = nullptr;
+    return ARC_OK;
+}
 
 uint32_t arc_session_prefill_kernels(const arc_session* s) { return s ? s->prefill_kernels : 0; }
 

@@ -66,6 +66,9 @@ struct arc_session {
     uint32_t kernels_per_step = 0;
     arc::PrefillBufs* pf = nullptr;  // batched prompt-pass buffers, made on first use
     uint32_t prefill_kernels = 0;    // launches of the last arc_session_prefill call
+    // per layer: EXEC148 image of a Q4_K ffn_down the decode step reads
+    // instead of the packed tensor (route B), or null (route A)
+    std::vector<const uint8_t*> down_e148;
 
     ~arc_session()
     {

@@ -11,14 +11,22 @@
  *    failure) throw std::runtime_error; nothing else escapes;
  *  - shader_dir must be non-empty as in the reference; the kernels are built
  *    into the library (libarcllm_hip.so), so its value is not read;
- *    sidecar_path, evidence_profile and request_within_validated_domain are
- *    accepted and not used by generation, as in the reference.
+ *  - the Q4_K ffn_down layers are routed per decode step by the Q4-down
+ *    policy (generic_policy_engine_v4.h) over the gfx950 registration, as in
+ *    the reference (src/arcllm_v1_runtime.cpp:305-337, 459-530):
+ *    evidence_profile picks the profile, request_within_validated_domain is
+ *    the capability's evidence scope (outside it, route A only),
+ *    sidecar_path names an EXEC148 family image for the P3 acquisition path;
+ *    an image acquired for a request is evicted when it ends.
  *
  * RuntimeStats: "dispatches" are kernel launches; decode "submits" are
  * captured-graph launches (one per step) and prefill "submits" are batched
- * prompt passes of up to 256 rows; route_a_steps counts decode steps run on the
- * direct packed kernels (route B, the EXEC148 repack, is not used), so
- * acquire/evict and the b_* / p* counters stay 0.
+ * prompt passes of up to 256 rows; route_a_steps / route_b_steps count decode
+ * steps on the packed Q4_K kernels / the EXEC148 image (a model without
+ * Q4_K ffn_down counts every step as route A), acquire_events /
+ * evict_events the policy's lifecycle actions, b_* and p* the backend's
+ * allocations, materializations, validations, releases and acquisition
+ * path calls.
  */
 #pragma once
 

@@ -259,6 +259,21 @@ int arc_session_prefill(arc_session *session, const uint32_t *tokens, uint32_t n
 /* Logits of the last step run with ARC_DECODE_LOGITS (host, vocab floats). */
 int arc_session_logits(arc_session *session, float *host_logits);
 uint32_t arc_session_kernels_per_step(const arc_session *session);
+
+/* Device pointer of a model tensor (layer < 0: the global tensors
+ * ARC_T_TOKEN_EMBD .. ARC_T_OUTPUT_NORM; otherwise slot `which` of `layer`),
+ * in the layout of arc_model_create.  Used by the Q4_K FFN-down backend to
+ * build the EXEC148 representation on the GPU. */
+int arc_model_tensor_device(const arc_model *model, int layer, int which, const void **ptr);
+
+/* Route B of the Q4_K FFN-down capability for one decode layer: the decode
+ * step of this session multiplies by `exec148` (the EXEC148 image of that
+ * layer's Q4_K ffn_down, see arc_exec148_materialize; 16-byte aligned, kept
+ * alive by the caller while routed) instead of the packed tensor; NULL
+ * returns the layer to route A.  A change takes effect at the next decode
+ * call (the captured step is rebuilt).  The reference's route selection,
+ * src/arcllm_v1_q4_vulkan_backend_v4_runtime.h:347-386 (append_ffn_down_op). */
+int arc_session_route_down(arc_session *session, uint32_t layer, const void *exec148);
 /* Kernel launches of the last arc_session_prefill call. */
 uint32_t arc_session_prefill_kernels(const arc_session *session);
 

@@ -14,14 +14,21 @@ oracle/_ref/libref.so from the reference sources where they lie:
                         (src/q4_down_exec148_materializer.h)
   sha256_kat.json       SHA-256 of "abc" and of a 148-block EXEC148 image via
                         the reference's Sha256 class
+  policy_trace.json     per-section case counts and FNV-1a-64 hashes of the
+                        decision trace of tests/cpp/policy_parity.cpp built
+                        against the reference's registry v2 / policy v4 /
+                        binding v4 / Q4-down registration sources
+                        (oracle/_ref/policy_parity_ref)
 
-Run: python tests/golden/make_golden.py   (needs oracle/_ref/libref.so)
+Run: python tests/golden/make_golden.py [policy]   (needs `make -C oracle ref`;
+"policy" rewrites policy_trace.json only)
 """
 from __future__ import annotations
 
 import ctypes as C
 import json
 import os
+import subprocess
 import sys
 
 import numpy as np
@@ -31,7 +38,23 @@ sys.path.insert(0, os.path.dirname(HERE))
 import oracle_lib as orc  # noqa: E402
 
 
+def policy_trace() -> None:
+    exe = os.path.join(os.path.dirname(os.path.dirname(HERE)), "oracle", "_ref", "policy_parity_ref")
+    if not os.path.exists(exe):
+        raise SystemExit("oracle/_ref/policy_parity_ref missing: run `make -C oracle ref` first")
+    out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout
+    sections = {}
+    for line in out.splitlines():
+        name, cases, fnv = line.split()
+        sections[name] = {"cases": int(cases.split("=")[1]), "fnv1a64": fnv.split("=")[1]}
+    with open(os.path.join(HERE, "policy_trace.json"), "w") as f:
+        json.dump({"program": "tests/cpp/policy_parity.cpp", "sections": sections}, f, indent=1)
+
+
 def main() -> None:
+    if sys.argv[1:] == ["policy"]:
+        policy_trace()
+        return
     if not orc.have_ref():
         raise SystemExit("oracle/_ref/libref.so missing: run `make -C oracle ref` first")
     R = orc.ref()
@@ -113,6 +136,9 @@ def main() -> None:
     with open(os.path.join(HERE, "sha256_kat.json"), "w") as f:
         json.dump({"abc": sha(b"abc"), "empty": sha(b""), "exec148_2rows": sha(bytes(ex148[:8].ravel()))},
                   f, indent=1)
+
+    # 5. plugin surface decision trace
+    policy_trace()
     print("golden vectors written to", HERE)
 
 
