@@ -86,6 +86,7 @@ _SIGS = {
     "arc_probe_read": [_P, C.c_size_t, _P, _U32, _P],
     "arc_exec148_materialize": [_P, _U32, _U32, _P, _P],
     "arc_exec148_validate": [_P, _P, _U32, _U32, C.POINTER(_U64), _P],
+    "arc_exec148_validate_many": [C.POINTER(_P), C.POINTER(_P), _U32, _U32, _U32, C.POINTER(_U64), _P],
 }
 _RESTYPE = {
     "arc_last_error": C.c_char_p,
@@ -124,6 +125,8 @@ _SIGS.update({
     "arc_session_logits": [_P, _P],
     "arc_session_kernels_per_step": [_P],
     "arc_session_prefill_kernels": [_P],
+    "arc_model_tensor_device": [_P, C.c_int, C.c_int, C.POINTER(_P)],
+    "arc_session_route_down": [_P, _U32, _P],
 })
 _RESTYPE.update({"arc_model_weight_bytes": _U64, "arc_session_kernels_per_step": _U32,
                  "arc_session_prefill_kernels": _U32})
@@ -149,6 +152,7 @@ def lib() -> C.CDLL:
 
 RUNTIME_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libarcllm_runtime.so")
 CLI_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "arcllm_runtime")
+Q4_PATHS_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "arcllm_q4_paths")
 _rt = None
 
 
@@ -341,6 +345,17 @@ def exec148_validate(q4, exec148, rows: int, K: int, stream: Optional[Stream] = 
     """Number of EXEC148 blocks that differ from the repack of their source (0 = exact)."""
     n = C.c_uint64(0)
     check(lib().arc_exec148_validate(_ptr(q4), _ptr(exec148), rows, K, C.byref(n), _sp(stream)))
+    return int(n.value)
+
+
+def exec148_validate_many(q4s, execs, rows: int, K: int, stream: Optional[Stream] = None) -> int:
+    """Mismatched EXEC148 blocks summed over the pairs (q4s[i], execs[i]) of one shape."""
+    if len(q4s) != len(execs):
+        raise ValueError("q4s and execs differ in length")
+    a = (C.c_void_p * len(q4s))(*[_ptr(x) for x in q4s])
+    b = (C.c_void_p * len(execs))(*[_ptr(x) for x in execs])
+    n = C.c_uint64(0)
+    check(lib().arc_exec148_validate_many(a, b, len(q4s), rows, K, C.byref(n), _sp(stream)))
     return int(n.value)
 
 

@@ -6,6 +6,8 @@
   ``arcllm_amd/host`` (GGUF reader, ``arcllm::v1::runtime::generate``),
   compiled with g++ against the C ABI only.
 * ``arcllm_amd/arcllm_runtime``: the command-line front end.
+* ``arcllm_amd/arcllm_q4_paths``: the Q4_K ffn_down route / EXEC148
+  acquisition path exerciser and timer.
 
 ``python -m arcllm_amd.build`` or ``__graft_entry__.build()`` runs it; it
 always recompiles.  Libraries and the CLI find each other through
@@ -26,7 +28,8 @@ LIB = os.path.join(PKG, "libarcllm_hip.so")
 HOST = os.path.join(PKG, "host")
 RUNTIME_LIB = os.path.join(PKG, "libarcllm_runtime.so")
 CLI = os.path.join(PKG, "arcllm_runtime")
-HOST_SOURCES = ["gguf.cpp", "runtime.cpp", "inspect.cpp", "registry_v2.cpp", "policy_v4.cpp", "binding_v4.cpp",
+Q4_PATHS = os.path.join(PKG, "arcllm_q4_paths")
+HOST_SOURCES = ["gguf.cpp", "qwen2_binding.cpp", "runtime.cpp", "inspect.cpp", "registry_v2.cpp", "policy_v4.cpp", "binding_v4.cpp",
                 "q4_down_backend.cpp", "registrations/arcllm_v1_q4k_down_reference_registration_v2.cpp"]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 ARCH = "gfx950"
@@ -96,8 +99,12 @@ def build_host(verbose: bool = True) -> None:
     _run([cxx, *HOST_FLAGS, "-o", tmp, os.path.join(HOST, "cli.cpp"), f"-L{PKG}", "-l:libarcllm_runtime.so",
           "-l:libarcllm_hip.so", rpath], "CLI")
     os.replace(tmp, CLI)
+    tmp = Q4_PATHS + ".tmp"
+    _run([cxx, *HOST_FLAGS, "-o", tmp, os.path.join(HOST, "q4_paths.cpp"), f"-L{PKG}", "-l:libarcllm_runtime.so",
+          "-l:libarcllm_hip.so", rpath], "Q4 path tool")
+    os.replace(tmp, Q4_PATHS)
     if verbose:
-        print(f"built {RUNTIME_LIB} and {CLI}")
+        print(f"built {RUNTIME_LIB}, {CLI} and {Q4_PATHS}")
 
 
 if __name__ == "__main__":

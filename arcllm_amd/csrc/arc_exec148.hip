@@ -9,13 +9,15 @@
 // elements 2p (low nibble) and 2p + 1 (high nibble).
 //
 // Both kernels are HBM-bound byte work.  A workgroup handles 256 consecutive
-// blocks: their 36,864 source bytes are read with coalesced 16-byte loads
-// into LDS, each thread repacks one block in registers into a second LDS
-// buffer (stride 37 dwords, conflict-free), and the 37,888 result bytes are
-// written back (repack) or read and compared (validation) with coalesced
-// accesses.  The validation compares whole blocks: an EXEC148 block's
-// canonical tuple (d and dmin bytes, the (sc, mn) bytes, every code nibble)
-// holds every bit of the block, so equal tuples mean equal bytes.
+// blocks, one per thread: each thread reads its 144-byte source block with
+// nine 16-byte loads (the workgroup's loads cover its 36,864 source bytes
+// contiguously), repacks it in registers and writes the 37 result dwords to
+// LDS at a 37-dword stride (odd: conflict-free); the workgroup's 37,888
+// result bytes then leave LDS in destination order with coalesced 16-byte
+// accesses, written (repack) or compared with the destination (validation).
+// The validation compares whole blocks: an EXEC148 block's canonical tuple
+// (d and dmin bytes, the (sc, mn) bytes, every code nibble) holds every bit
+// of the block, so equal tuples mean equal bytes.
 #include "arc_device.hpp"
 #include "../../include/arcllm_hip.h"
 
@@ -38,8 +40,8 @@ constexpr uint32_t kDstWords = kE148Bytes / 4;           // 37 dwords per EXEC14
 // lanes): byte i of the result pair is n_{2i} | n_{2i+1} << 4 (in bytes 0, 2).
 __device__ __forceinline__ uint32_t pair_nibbles(uint32_t n) { return (n | (n >> 4)) & 0x00ff00ffu; }
 
-// Repack of the block at LDS words `in` (36 dwords) into `out` (37 dwords).
-__device__ __forceinline__ void repack_block(const uint32_t* in, uint32_t* out)
+// The EXEC148 block of the Q4_K block held in `in` (36 dwords) as 37 dwords.
+__device__ __forceinline__ void repack_block(const uint32_t (&in)[36], uint32_t* out)
 {
     out[0] = in[0];  // d, dmin
     const uint32_t s0 = in[1], s1 = in[2], s2 = in[3];  // scale bytes 4..15
@@ -74,19 +76,22 @@ __device__ __forceinline__ void repack_block(const uint32_t* in, uint32_t* out)
         }
 }
 
-// Stages the workgroup's source blocks and repacks them into `out_lds`;
-// returns the number of blocks of this workgroup.
-__device__ __forceinline__ uint32_t stage_and_repack(const uint8_t* __restrict__ src, uint64_t nblocks,
-                                                     u32x4* in_lds, uint32_t* out_lds)
+// Repacks this thread's block into out_lds (37-dword stride); returns the
+// number of blocks of the workgroup.
+__device__ __forceinline__ uint32_t repack_to_lds(const uint8_t* __restrict__ src, uint64_t nblocks, uint32_t* out_lds)
 {
     const uint64_t b0 = uint64_t(blockIdx.x) * kE148PerWg;
     const uint32_t nb = uint32_t(min(uint64_t(kE148PerWg), nblocks - b0));
-    const u32x4* g = reinterpret_cast<const u32x4*>(src + b0 * kQ4Bytes);
-    for (uint32_t i = threadIdx.x; i < nb * kSrcPieces; i += kE148PerWg) in_lds[i] = g[i];
-    __syncthreads();
-    if (threadIdx.x < nb)
-        repack_block(reinterpret_cast<const uint32_t*>(in_lds + threadIdx.x * kSrcPieces),
-                     out_lds + threadIdx.x * kDstWords);
+    if (threadIdx.x < nb) {
+        const u32x4* g = reinterpret_cast<const u32x4*>(src + (b0 + threadIdx.x) * kQ4Bytes);
+        uint32_t in[36];
+#pragma unroll
+        for (uint32_t p = 0; p < kSrcPieces; ++p) {
+            const u32x4 v = g[p];
+            in[4 * p] = v.x, in[4 * p + 1] = v.y, in[4 * p + 2] = v.z, in[4 * p + 3] = v.w;
+        }
+        repack_block(in, out_lds + threadIdx.x * kDstWords);
+    }
     __syncthreads();
     return nb;
 }
@@ -94,12 +99,10 @@ __device__ __forceinline__ uint32_t stage_and_repack(const uint8_t* __restrict__
 __global__ __launch_bounds__(256) void k_exec148_materialize(const uint8_t* __restrict__ src, uint64_t nblocks,
                                                              uint8_t* __restrict__ dst)
 {
-    __shared__ u32x4 in_lds[kE148PerWg * kSrcPieces];
     __shared__ __align__(16) uint32_t out_lds[kE148PerWg * kDstWords];
-    const uint32_t nb = stage_and_repack(src, nblocks, in_lds, out_lds);
-    const uint64_t b0 = uint64_t(blockIdx.x) * kE148PerWg;
+    const uint32_t nb = repack_to_lds(src, nblocks, out_lds);
     // the workgroup's destination starts at a multiple of 256 * 148 bytes (16-byte aligned)
-    uint32_t* g = reinterpret_cast<uint32_t*>(dst + b0 * kE148Bytes);
+    uint32_t* g = reinterpret_cast<uint32_t*>(dst + uint64_t(blockIdx.x) * kE148PerWg * kE148Bytes);
     const uint32_t words = nb * kDstWords, quads = words / 4;
     for (uint32_t i = threadIdx.x; i < quads; i += kE148PerWg)
         reinterpret_cast<u32x4*>(g)[i] = reinterpret_cast<const u32x4*>(out_lds)[i];
@@ -112,15 +115,20 @@ __global__ __launch_bounds__(256) void k_exec148_validate(const uint8_t* __restr
                                                           const uint8_t* __restrict__ exec, uint64_t nblocks,
                                                           unsigned long long* __restrict__ mismatched)
 {
-    __shared__ u32x4 in_lds[kE148PerWg * kSrcPieces];
     __shared__ __align__(16) uint32_t out_lds[kE148PerWg * kDstWords];
     __shared__ uint32_t bad[kE148PerWg];
-    const uint32_t nb = stage_and_repack(src, nblocks, in_lds, out_lds);
-    const uint64_t b0 = uint64_t(blockIdx.x) * kE148PerWg;
     bad[threadIdx.x] = 0;
-    __syncthreads();
-    const uint32_t* g = reinterpret_cast<const uint32_t*>(exec + b0 * kE148Bytes);
-    for (uint32_t i = threadIdx.x; i < nb * kDstWords; i += kE148PerWg)
+    const uint32_t nb = repack_to_lds(src, nblocks, out_lds);
+    const uint32_t* g = reinterpret_cast<const uint32_t*>(exec + uint64_t(blockIdx.x) * kE148PerWg * kE148Bytes);
+    const uint32_t words = nb * kDstWords, quads = words / 4;
+    for (uint32_t i = threadIdx.x; i < quads; i += kE148PerWg) {
+        const u32x4 x = reinterpret_cast<const u32x4*>(g)[i], y = reinterpret_cast<const u32x4*>(out_lds)[i];
+        if (x.x != y.x) bad[(4 * i) / kDstWords] = 1;
+        if (x.y != y.y) bad[(4 * i + 1) / kDstWords] = 1;
+        if (x.z != y.z) bad[(4 * i + 2) / kDstWords] = 1;
+        if (x.w != y.w) bad[(4 * i + 3) / kDstWords] = 1;
+    }
+    for (uint32_t i = quads * 4 + threadIdx.x; i < words; i += kE148PerWg)
         if (g[i] != out_lds[i]) bad[i / kDstWords] = 1;
     __syncthreads();
     const uint32_t n = uint32_t(__syncthreads_count(threadIdx.x < nb && bad[threadIdx.x] != 0));
@@ -163,21 +171,25 @@ int arc_exec148_materialize(const void* q4, uint32_t rows, uint32_t K, void* exe
     return check_hip(hipGetLastError(), "exec148 materialize");
 }
 
-int arc_exec148_validate(const void* q4, const void* exec, uint32_t rows, uint32_t K, uint64_t* mismatched,
-                         arc_stream_t stream)
+int arc_exec148_validate_many(const void* const* q4, const void* const* exec, uint32_t count, uint32_t rows,
+                              uint32_t K, uint64_t* mismatched, arc_stream_t stream)
 {
+    if (!q4 || !exec || !mismatched || count == 0) return set_error(ARC_ERR_INVALID_ARGUMENT, "bad validate arguments");
     uint64_t nb = 0;
-    int rc = check_e148(q4, rows, K, exec, nb);
-    if (rc) return rc;
-    if (!mismatched) return set_error(ARC_ERR_INVALID_ARGUMENT, "null result pointer");
+    for (uint32_t i = 0; i < count; ++i) {
+        const int rc = check_e148(q4[i], rows, K, exec[i], nb);
+        if (rc) return rc;
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
     unsigned long long* cnt = nullptr;
-    if ((rc = check_hip(hipMalloc(reinterpret_cast<void**>(&cnt), sizeof(*cnt)), "exec148 validate counter"))) return rc;
+    int rc = check_hip(hipMalloc(reinterpret_cast<void**>(&cnt), sizeof(*cnt)), "exec148 validate counter");
+    if (rc) return rc;
     unsigned long long host = 0;
     rc = check_hip(hipMemcpyAsync(cnt, &host, sizeof(host), hipMemcpyHostToDevice, s), "exec148 validate clear");
-    if (!rc) {
+    // one counter for every tensor, one synchronization at the end
+    for (uint32_t i = 0; i < count && !rc; ++i) {
         hipLaunchKernelGGL(k_exec148_validate, dim3(uint32_t((nb + kE148PerWg - 1) / kE148PerWg)), dim3(kE148PerWg),
-                           0, s, static_cast<const uint8_t*>(q4), static_cast<const uint8_t*>(exec), nb, cnt);
+                           0, s, static_cast<const uint8_t*>(q4[i]), static_cast<const uint8_t*>(exec[i]), nb, cnt);
         rc = check_hip(hipGetLastError(), "exec148 validate");
     }
     if (!rc) rc = check_hip(hipMemcpyAsync(&host, cnt, sizeof(host), hipMemcpyDeviceToHost, s), "exec148 validate result");
@@ -185,6 +197,12 @@ int arc_exec148_validate(const void* q4, const void* exec, uint32_t rows, uint32
     (void)hipFree(cnt);
     if (!rc) *mismatched = host;
     return rc;
+}
+
+int arc_exec148_validate(const void* q4, const void* exec, uint32_t rows, uint32_t K, uint64_t* mismatched,
+                         arc_stream_t stream)
+{
+    return arc_exec148_validate_many(&q4, &exec, 1, rows, K, mismatched, stream);
 }
 
 }  // extern "C"

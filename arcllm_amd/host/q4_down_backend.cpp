@@ -80,17 +80,18 @@ void exec148_repack_host(const std::uint8_t* q4, std::uint32_t rows, std::uint32
 
 namespace {
 
-// Future decode tokens from which each path pays for itself on MI355X
-// (Qwen2.5-7B Q4_K_M shape, ffn_down 3584 x 18944):
-//   saving per token and Q4_K ffn_down layer = route A - route B
-//     (23.15 us - 17.56 us = 5.59 us, split-K GEMVs timed with HIP events);
-//   P1 cost per layer = allocation share + GPU repack + GPU validation;
-//   P3 cost per layer = sidecar read + upload + validation;
-//   P0 cost per layer = host repack + upload + validation;
-// threshold = ceil(cost / saving).  Profile 1 doubles profile 0 as the
-// reference's conservative profile does (src/registrations/
+// Future decode tokens from which each path pays for itself on MI355X,
+// measured with arcllm_q4_paths on the Qwen2.5-7B shape with the 14 Q4_K
+// ffn_down layers of its Q4_K_M file (family image 549,527,552 bytes):
+//   saving per decode token, route B over route A: 61.4 us (28-layer step,
+//     2.020 -> 1.959 ms at context 512);
+//   P1: allocation + GPU repack 1.55 ms, GPU validation 0.45 ms -> 33;
+//   P3: sidecar read (page cache dropped) + upload ~98 ms + validation -> 1600;
+//   P0: host repack (16 threads) + upload ~78 ms + validation -> 1300;
+// threshold = ceil(cost / saving).  Profile 1 doubles profile 0, as the
+// reference's conservative profile roughly does (src/registrations/
 // arcllm_v1_q4k_down_reference_registration_v2.cpp:39-46: 2/4, 15/33, 17/37).
-constexpr std::array<std::uint64_t, 6> kThresholds = {12, 600, 1400, 24, 1200, 2800};
+constexpr std::array<std::uint64_t, 6> kThresholds = {33, 1600, 1300, 66, 3200, 2600};
 
 constexpr reg::ProvenanceRef kMeasured{"profiles/q4_down_routes_mi355x.md", nullptr};
 constexpr auto V = reg::ValidationState::VALIDATED;
@@ -287,16 +288,19 @@ bind::BackendStatus HipQ4DownBackend::validate(bind::RepresentationHandle repres
         return bind::BackendStatus::INVALID_BINDING_STATE;
     ++counters_.b_validations;
     validated_ = false;
-    std::uint64_t total = 0;
+    std::vector<const void*> src(layers_.size()), img(layers_.size());
     for (std::size_t i = 0; i < layers_.size(); ++i) {
-        const void* src = nullptr;
-        std::uint64_t bad = 0;
-        if (arc_model_tensor_device(model_, int(layers_[i]), ARC_T_FFN_DOWN, &src) != ARC_OK ||
-            arc_exec148_validate(src, exec_ + i * slot_stride_, rows_, K_, &bad, nullptr) != ARC_OK) {
+        if (arc_model_tensor_device(model_, int(layers_[i]), ARC_T_FFN_DOWN, &src[i]) != ARC_OK) {
             last_error_ = arc_last_error();
             return bind::BackendStatus::VALIDATION_FAILED;
         }
-        total += bad;
+        img[i] = exec_ + i * slot_stride_;
+    }
+    std::uint64_t total = 0;
+    if (arc_exec148_validate_many(src.data(), img.data(), std::uint32_t(layers_.size()), rows_, K_, &total, nullptr) !=
+        ARC_OK) {
+        last_error_ = arc_last_error();
+        return bind::BackendStatus::VALIDATION_FAILED;
     }
     last_mismatched_ = total;
     if (total) {

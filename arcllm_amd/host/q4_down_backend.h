@@ -104,6 +104,11 @@ public:
     bool validated() const noexcept { return validated_; }
     bool p3_available() const noexcept;
     std::uint64_t family_bytes() const noexcept { return family_bytes_; }
+    /* the device image while resident: layer i's EXEC148 bytes (layer_bytes())
+     * at device_image() + i * slot_stride() */
+    const std::uint8_t* device_image() const noexcept { return exec_; }
+    std::uint64_t layer_bytes() const noexcept { return layer_bytes_; }
+    std::uint64_t slot_stride() const noexcept { return slot_stride_; }
     const std::vector<std::uint32_t>& layers() const noexcept { return layers_; }
     const BackendCounters& counters() const noexcept { return counters_; }
     std::uint64_t last_mismatched_blocks() const noexcept { return last_mismatched_; }

@@ -131,6 +131,13 @@ int arc_exec148_materialize(const void *q4, uint32_t rows, uint32_t K, void *exe
  * (src/q4_down_exec148_materializer.h:21-22); synchronous on `stream`. */
 int arc_exec148_validate(const void *q4, const void *exec, uint32_t rows, uint32_t K, uint64_t *mismatched,
                          arc_stream_t stream);
+/* The same check over `count` tensor pairs of one shape (q4[i] against
+ * exec[i]) with one result: *mismatched = mismatched blocks over all pairs;
+ * one synchronization (the whole family of a model in one call, as
+ * validate_image does for its 14 layers,
+ * src/arcllm_v1_q4_vulkan_backend_v4_runtime.h:97-119). */
+int arc_exec148_validate_many(const void *const *q4, const void *const *exec, uint32_t count, uint32_t rows,
+                              uint32_t K, uint64_t *mismatched, arc_stream_t stream);
 
 /* ------------------------------------------------------- norm / LM head */
 /* y = x * rsqrt(mean(x^2) + eps) * w over n elements (shaders/p7_rmsnorm_seq.comp). */

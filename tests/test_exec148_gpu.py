@@ -87,6 +87,25 @@ def test_validate_exact_and_planted_mismatches():
     assert arc.exec148_validate(wd, dev(bad.ravel()), rows, K) == len(planted)
 
 
+def test_validate_many_sums_over_tensors():
+    """Several tensor pairs in one call: exact images count 0, planted blocks
+    in two of them are summed, a swapped pair (image of another tensor)
+    mismatches on every block."""
+    rows, K = 40, 768
+    ws = [q4(rows, K, 20 + i) for i in range(3)]
+    wd = [dev(w) for w in ws]
+    es = [gpu_exec148(w, rows, K) for w in ws]
+    assert arc.exec148_validate_many(wd, es, rows, K) == 0
+    nb = rows * (K // 256)
+    imgs = [e.download(np.uint8).reshape(-1, 148).copy() for e in es]
+    imgs[0][7, 25] ^= 0x10
+    imgs[2][0, 2] ^= 0x01
+    imgs[2][nb - 1, 147] ^= 0x80
+    bad = [dev(im.ravel()) for im in imgs]
+    assert arc.exec148_validate_many(wd, bad, rows, K) == 3
+    assert arc.exec148_validate_many([wd[1], wd[0]], [es[0], es[1]], rows, K) == 2 * nb
+
+
 @pytest.mark.parametrize("rows,K", [(64, 512), (1000, 3584), (3584, 18944)])
 def test_route_b_gemv(rows, K):
     w = q4(rows, K, 3)

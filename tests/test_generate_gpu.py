@@ -7,6 +7,7 @@ Token comparison uses the near-tie rule of test_decode_gpu.py (a differing
 step must be a top-2 tie within 2e-3 * max|logit| and ends the comparison).
 """
 import json
+import os
 import subprocess
 import sys
 
@@ -58,13 +59,19 @@ def _gpu():
     assert arc.device_count() >= 1, "no HIP device visible"
 
 
+def thresholds():
+    """The gfx950 registration's reuse thresholds (future decode tokens)."""
+    r = subprocess.run([arc.Q4_PATHS_PATH, "--thresholds"], capture_output=True, text=True, timeout=30, check=True)
+    return json.loads(r.stdout)
+
+
 def test_generate_cli_matches_oracle(tmp_path):
     d = tiny_dims(layers=3)
     T = arc.synth_model_tensors(d, SEED)
     path = str(tmp_path / "model.gguf")
     gw.write_qwen2_model(path, d, T)
     prompt = [17, 5, 900, 33, 2048, 7, 4095]
-    max_new = 24
+    max_new = thresholds()["profile0"]["p1"] + 3
     r = subprocess.run([arc.CLI_PATH, "--model", path, "--shader-dir", "builtin", "--tokens",
                         ",".join(map(str, prompt)), "--max-new", str(max_new), "--profile", "0",
                         "--within-validated-domain", "1"], capture_output=True, text=True, timeout=120)
@@ -81,8 +88,94 @@ def test_generate_cli_matches_oracle(tmp_path):
     # batched prompt pass: embed + first norm, 8 launches per layer, LM head + next token
     assert st["prefill_dispatches"] == 8 * d.layers + 4 and st["prefill_submits"] == 1
     assert st["decode_dispatches_per_step"] == per_step and st["decode_submits_per_step"] == 1
-    assert st["decode_steps"] == max_new - 1 and st["route_a_steps"] == max_new - 1
-    assert st["route_b_steps"] == 0 and st["finite"] is True
+    # layer 1's ffn_down is Q4_K: within the evidence scope and with
+    # max_new - 1 future tokens (>= the P1 threshold) the policy acquires the EXEC148 image by P1
+    # before the first decode step, every step runs route B, and the close
+    # decision evicts it
+    assert st["decode_steps"] == max_new - 1 and st["route_b_steps"] == max_new - 1
+    assert st["route_a_steps"] == 0 and st["finite"] is True
+    assert st["acquire_events"] == 1 and st["evict_events"] == 1
+    assert (st["b_allocations"], st["b_materializations"], st["b_validations"], st["b_releases"]) == (1, 1, 1, 1)
+    assert (st["p1_calls"], st["p3_calls"], st["p0_calls"]) == (1, 0, 0)
+
+
+def _q4_model(tmp_path, layers, seed):
+    d = tiny_dims(layers=layers)
+    T = arc.synth_model_tensors(d, seed)
+    path = str(tmp_path / "q4.gguf")
+    gw.write_qwen2_model(path, d, T)
+    return d, T, path
+
+
+def _cli(path, prompt, max_new, profile, scope, sidecar=None):
+    cmd = [arc.CLI_PATH, "--model", path, "--shader-dir", "builtin", "--tokens", ",".join(map(str, prompt)),
+           "--max-new", str(max_new), "--profile", str(profile), "--within-validated-domain", str(scope)]
+    if sidecar:
+        cmd += ["--sidecar", sidecar]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    return json.loads(r.stdout)
+
+
+def test_generate_routes_by_scope_and_reuse(tmp_path):
+    """Route A outside the evidence scope or below the P1 threshold of the
+    profile; route B from the threshold on (max_new - 1 future tokens at the
+    first decode step), with the same tokens as the oracle either way."""
+    d, T, path = _q4_model(tmp_path, 2, SEED + 7)
+    prompt = [5, 77, 1024]
+    th = thresholds()
+    t0, t1 = th["profile0"]["p1"], th["profile1"]["p1"]
+    longest = t1 + 2
+    ref, second, margins, scale = oracle_generate(d, T, prompt, longest)
+    cases = [  # (max_new, profile, scope, route B expected)
+        (longest, 0, 0, False), (t0, 0, 1, False), (t0 + 1, 0, 1, True), (t1, 1, 1, False), (t1 + 1, 1, 1, True)]
+    for max_new, prof, scope, route_b in cases:
+        _log(f"case max_new={max_new} profile={prof} scope={scope}")
+        res = _cli(path, prompt, max_new, prof, scope)
+        st = res["stats"]
+        steps = max_new - 1
+        assert st["decode_steps"] == steps
+        if route_b:
+            assert (st["route_a_steps"], st["route_b_steps"]) == (0, steps)
+            assert (st["acquire_events"], st["evict_events"], st["p1_calls"], st["b_releases"]) == (1, 1, 1, 1)
+        else:
+            assert (st["route_a_steps"], st["route_b_steps"]) == (steps, 0)
+            assert (st["acquire_events"], st["evict_events"], st["b_allocations"]) == (0, 0, 0)
+        assert tokens_match(res["generated_token_ids"], ref[:max_new], second, margins, scale) >= max_new // 2
+
+
+def test_q4_paths_tool_all_acquisition_paths(tmp_path):
+    """P1 (GPU repack), P3 (sidecar written from the P1 image) and P0 (host
+    repack) give the same EXEC148 image, equal to the oracle's repack of the
+    layers' Q4_K tensors, validated with zero mismatched blocks; route A and
+    route B decode the same tokens as the oracle from a prefilled KV cache."""
+    d, T, path = _q4_model(tmp_path, 3, SEED + 8)
+    ctx, steps, kv_seed = 40, 12, 77
+    sidecar = str(tmp_path / "family.e148")
+    r = subprocess.run([arc.Q4_PATHS_PATH, "--model", path, "--ctx", str(ctx), "--steps", str(steps),
+                        "--paths", "p1,p3,p0", "--sidecar", sidecar, "--seed", str(kv_seed - 1)],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    res = json.loads(r.stdout)
+    _log(json.dumps({k: v for k, v in res.items() if k != "route_a"}))
+    q4_layers = [layer for layer in range(d.layers) if d.down_type[layer] == arc.Q4_K]
+    assert res["q4_layers"] == q4_layers
+    image = np.concatenate([orc.exec148(T[3 + 12 * layer + 11], d.hidden, d.ffn) for layer in q4_layers])
+    assert res["family_bytes"] == image.size
+    h = 1469598103934665603
+    for b in image.tobytes():
+        h = ((h ^ b) * 1099511628211) & 0xFFFFFFFFFFFFFFFF
+    want = f"{h:016x}"
+    for p in ("p1", "p3", "p0"):
+        assert res["paths"][p]["mismatched_blocks"] == 0
+        assert res["paths"][p]["image_fnv"] == want, p
+    assert res["images_equal"] is True
+    assert os.path.getsize(sidecar) == image.size
+    o = orc.DecodeOracle(d, T, ctx + steps + 2)
+    o.fill_kv(ctx, kv_seed, arc.synth_normal)
+    ref, second, margins, scale = o.greedy(1234, ctx, steps)
+    for route in ("route_a", "route_b"):
+        assert tokens_match(res[route]["tokens"], ref, second, margins, scale) >= steps // 2, route
 
 
 def test_generate_single_token_request(tmp_path):
