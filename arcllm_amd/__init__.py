@@ -453,6 +453,12 @@ class Model:
     def weight_bytes(self) -> int:
         return int(lib().arc_model_weight_bytes(self.handle))
 
+    def tensor_device(self, layer: int, which: int) -> int:
+        """Device address of a resident tensor (layer -1: the global slots)."""
+        ptr = _P()
+        check(lib().arc_model_tensor_device(self.handle, layer, which, C.byref(ptr)))
+        return int(ptr.value)
+
     def close(self) -> None:
         if getattr(self, "handle", None):
             if _lib is not None:
@@ -478,6 +484,11 @@ class Session:
 
     def fill_kv(self, ctx: int, seed: int) -> None:
         check(lib().arc_session_fill_kv(self.handle, ctx, seed))
+
+    def route_down(self, layer: int, exec148=None) -> None:
+        """Route layer's Q4_K ffn_down to an EXEC148 image (route B; kept alive by
+        the caller) or, with None, back to the packed tensor (route A)."""
+        check(lib().arc_session_route_down(self.handle, layer, _ptr(exec148)))
 
     def kv(self, layer: int) -> tuple[int, int]:
         k, v = _P(), _P()
