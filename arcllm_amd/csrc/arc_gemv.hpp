@@ -87,13 +87,21 @@ struct GemvParams {
 };
 
 // ------------------------------------------------------------ block loads
+// The header is read as the d/dmin dword and the 12 scale bytes separately:
+// held as one 16-byte register tuple, its parts live for different times and
+// the register allocator copied them out right after the load, a copy that
+// waits for the load (the prefetch a block ahead then gains nothing).
+typedef uint32_t u32x3a4 __attribute__((ext_vector_type(3), aligned(4)));
 struct Q4Blk {
-    uint4 hdr, qa, qb;
+    uint32_t dm;    // d | dmin << 16
+    u32x3a4 sc;     // the 12 packed 6-bit scale/min bytes
+    uint4 qa, qb;
 };
 
 __device__ __forceinline__ void q4_load(const uint8_t* blk, int v, Q4Blk& o)
 {
-    o.hdr = ld16_aligned(blk);
+    o.dm = *reinterpret_cast<const uint32_t*>(blk);
+    o.sc = *reinterpret_cast<const u32x3a4*>(blk + opaque(4u));  // kept apart from the dword before it
     o.qa = ld16_aligned(blk + 16 + v * 16);
     o.qb = ld16_aligned(blk + 80 + v * 16);
 }
@@ -268,7 +276,7 @@ __device__ __forceinline__ void q4_dot(const Q4Blk (&b)[N], const float* xs, int
 #pragma unroll
     for (int n = 0; n < N; ++n) {
         // bytes of sc/mn for this lane's sub-blocks (2g, 2g+1, 2g+4, 2g+5), g = v>>1
-        const uint32_t yy = b[n].hdr.y >> sh, zz = b[n].hdr.z >> sh, ww = b[n].hdr.w >> sh;
+        const uint32_t yy = b[n].sc.x >> sh, zz = b[n].sc.y >> sh, ww = b[n].sc.z >> sh;
         const uint32_t SC = (yy & 0x3f3fu) | (((ww & 0x0f0fu) | ((yy >> 2) & 0x3030u)) << 16);
         const uint32_t MN = (zz & 0x3f3fu) | ((((ww >> 4) & 0x0f0fu) | ((zz >> 2) & 0x3030u)) << 16);
         float qs = byte_f(SC, 0) * a[n][0];
@@ -279,8 +287,8 @@ __device__ __forceinline__ void q4_dot(const Q4Blk (&b)[N], const float* xs, int
         ms = __builtin_fmaf(byte_f(MN, 1), S.y, ms);
         ms = __builtin_fmaf(byte_f(MN, 2), S.z, ms);
         ms = __builtin_fmaf(byte_f(MN, 3), S.w, ms);
-        acc[n] = fmix(b[n].hdr.x, false, qs, acc[n]);   // + d * qs
-        acc[n] = fmix(b[n].hdr.x, true, -ms, acc[n]);   // - dmin * ms
+        acc[n] = fmix(b[n].dm, false, qs, acc[n]);   // + d * qs
+        acc[n] = fmix(b[n].dm, true, -ms, acc[n]);   // - dmin * ms
     }
 }
 
@@ -806,23 +814,27 @@ __global__ __launch_bounds__(W * kWave) void k_gemv(GemvParams p)
     };
 
     uint32_t ci = 0, cj = 0;  // item being consumed
-    for (uint32_t s = 0; s < S; s += PF) {
-        bool done = false;
-#pragma unroll
-        for (int u = 0; u < PF; ++u) {
-            if (!done) {
-                load_next(buf[(u + PF - 1) % PF]);
-                compute(cj, buf[u]);
-                if constexpr (EPI == EPI_COLPART)
-                    finish_column(ci, cj);
-                else if (cj == nj - 1)
-                    finish(ci);
-                if (s + u + 1 >= S) done = true;
-                advance(ci, cj);
-            }
-        }
-        if (done) break;
+    auto step = [&](Blk (&next)[N], const Blk (&cur)[N]) {
+        load_next(next);
+        compute(cj, cur);
+        if constexpr (EPI == EPI_COLPART)
+            finish_column(ci, cj);
+        else if (cj == nj - 1)
+            finish(ci);
+        advance(ci, cj);
+    };
+    // Whole rounds of the ring as straight-line code with no exit between
+    // its items, so each buffer keeps its registers: when the items sat
+    // behind a per-item exit test, the compiler folded them into one item per
+    // iteration with copies between the buffers, and copying a buffer just
+    // loaded waited for its loads, losing the prefetch.
+    static_assert(PF == 2, "the ring is written out for two buffers");
+    uint32_t s = 0;
+    for (; s + PF <= S; s += PF) {
+        step(buf[1], buf[0]);
+        step(buf[0], buf[1]);
     }
+    if (s < S) step(buf[1], buf[0]);
 
     if constexpr (EPI == EPI_ARGMAX) wg_argmax(best_v, best_i, nonfinite, p.best + blockIdx.x);
 }
