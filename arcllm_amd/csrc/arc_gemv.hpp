@@ -106,30 +106,41 @@ __device__ __forceinline__ void q4_load(const uint8_t* blk, int v, Q4Blk& o)
     o.qb = ld16_aligned(blk + 80 + v * 16);
 }
 
+// A Q6_K block starts 0 or 2 bytes past a dword boundary.  Each 16-byte
+// chunk is read as a dwordx4 plus the following dword from the dword-aligned
+// block base and kept as read; q6_dot realigns it (by sh bytes) where it is
+// consumed, so nothing waits for a load right after issuing it.  The dwords
+// read cover block bytes [o-2, o+18) for o <= 192: each one holds at least one
+// byte of the block itself, so no read reaches a page the tensor does not
+// touch.  Pieces: 0, 1 ql of both 128-element halves, 2, 3 the matching qh,
+// 4 the int8 scales (its trailing dword holds d).
 struct Q6Blk {
-    uint32_t ql[2][4];
-    uint32_t qh[2][4];
-    uint32_t sc[4];
-    uint32_t d;
+    uint32_t w[5][5];
+    uint32_t sh;
 };
 
-// A Q6_K block starts 0 or 2 bytes past a dword boundary.  Every chunk offset
-// used here is a multiple of 4, so each chunk is read as a dwordx4 plus one
-// dword from the dword-aligned block base and shifted in registers.  The
-// dwords read cover block bytes [o-2, o+18) for o <= 192: each one holds at
-// least one byte of the block itself, so no read reaches a page the tensor
-// does not touch.
 __device__ __forceinline__ void q6_load(const uint8_t* blk, int v, Q6Blk& o)
 {
     const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(blk)) & 3u;
     const uint8_t* b = blk - sh;
-    uint32_t t;
-    ld16_shifted(b + v * 16, sh, o.ql[0], t);
-    ld16_shifted(b + 64 + v * 16, sh, o.ql[1], t);
-    ld16_shifted(b + 128 + (v & 1) * 16, sh, o.qh[0], t);
-    ld16_shifted(b + 160 + (v & 1) * 16, sh, o.qh[1], t);
-    ld16_shifted(b + 192, sh, o.sc, t);
-    o.d = t & 0xffffu;
+    const uint32_t off[5] = {uint32_t(v) * 16u, 64u + uint32_t(v) * 16u, 128u + uint32_t(v & 1) * 16u,
+                             160u + uint32_t(v & 1) * 16u, 192u};
+#pragma unroll
+    for (int p = 0; p < 5; ++p) {
+        const u32x4a4 x = *reinterpret_cast<const u32x4a4*>(b + off[p]);
+        o.w[p][0] = x.x;
+        o.w[p][1] = x.y;
+        o.w[p][2] = x.z;
+        o.w[p][3] = x.w;
+        o.w[p][4] = *reinterpret_cast<const uint32_t*>(b + off[p] + 16);
+    }
+    o.sh = sh;
+}
+
+// dword i of piece p of the block itself
+__device__ __forceinline__ uint32_t q6w(const Q6Blk& b, int p, int i)
+{
+    return __builtin_amdgcn_alignbyte(b.w[p][i + 1], b.w[p][i], b.sh);
 }
 
 // EXEC148 block (148 bytes, 4-byte aligned): bytes 0..3 d, dmin; 4 + 2j,
@@ -312,7 +323,7 @@ __device__ __forceinline__ void q6_dot(const Q6Blk (&b)[N], const float* xs, int
             const float4 xb = lds4(xs + (2 * h + 1) * 16 + dw * 4);
 #pragma unroll
             for (int n = 0; n < N; ++n) {
-                const uint32_t ql = b[n].ql[h][dw], qh = b[n].qh[h][dw];
+                const uint32_t ql = q6w(b[n], h, dw), qh = q6w(b[n], 2 + h, dw);
                 const uint32_t ua = (ql & 0x0f0f0f0fu) | ((qh << s1) & 0x30303030u);
                 const uint32_t ub = ((ql >> 4) & 0x0f0f0f0fu) | ((qh >> s2) & 0x30303030u);
                 mix4x2(ua, xa, a[n][2 * h], ub, xb, a[n][2 * h + 1]);
@@ -324,11 +335,12 @@ __device__ __forceinline__ void q6_dot(const Q6Blk (&b)[N], const float* xs, int
     const uint32_t i0 = 8u * ((v & 1) + 2 * qa);
 #pragma unroll
     for (int n = 0; n < N; ++n) {
-        float t = float(int8_t(uint8_t(b[n].sc[0] >> i0))) * __builtin_fmaf(-32.0f, S.x, a[n][0]);
-        t = __builtin_fmaf(float(int8_t(uint8_t(b[n].sc[1] >> i0))), __builtin_fmaf(-32.0f, S.y, a[n][1]), t);
-        t = __builtin_fmaf(float(int8_t(uint8_t(b[n].sc[2] >> i0))), __builtin_fmaf(-32.0f, S.z, a[n][2]), t);
-        t = __builtin_fmaf(float(int8_t(uint8_t(b[n].sc[3] >> i0))), __builtin_fmaf(-32.0f, S.w, a[n][3]), t);
-        acc[n] = fmix(b[n].d, false, t, acc[n]);  // + d * t
+        float t = float(int8_t(uint8_t(q6w(b[n], 4, 0) >> i0))) * __builtin_fmaf(-32.0f, S.x, a[n][0]);
+        t = __builtin_fmaf(float(int8_t(uint8_t(q6w(b[n], 4, 1) >> i0))), __builtin_fmaf(-32.0f, S.y, a[n][1]), t);
+        t = __builtin_fmaf(float(int8_t(uint8_t(q6w(b[n], 4, 2) >> i0))), __builtin_fmaf(-32.0f, S.z, a[n][2]), t);
+        t = __builtin_fmaf(float(int8_t(uint8_t(q6w(b[n], 4, 3) >> i0))), __builtin_fmaf(-32.0f, S.w, a[n][3]), t);
+        const uint32_t d = b[n].w[4][4] >> (8u * b[n].sh);  // bytes 208, 209 in the low half
+        acc[n] = fmix(d, false, t, acc[n]);  // + d * t
     }
 }
 
@@ -675,33 +687,42 @@ __global__ __launch_bounds__(W * kWave) void k_gemv(GemvParams p)
 #pragma unroll
     for (int u = 0; u < PF - 1; ++u) load_next(buf[u]);
 
-    // epilogue operands of the wave's first tile, fetched under the staging
-    float pre_b[RPL], pre_r[RPL];
-    float2 pre_cs = {1.0f, 0.0f};
+    // Epilogue operands (bias, residual, accumulated output, RoPE factors) of
+    // the tile being consumed, loaded at its first item ahead of that item's
+    // prefetch: the epilogue then waits only for loads issued before the
+    // prefetch, not for the prefetch itself (the load counter is in order).
+    // The first tile's are fetched under the x staging.
+    float ep_b[RPL], ep_r[RPL], ep_y[RPL];
+    float2 ep_cs = {1.0f, 0.0f};
     uint32_t pos = 0;
-    {
-        const uint32_t tile0 = min(gw, p.ntiles - 1);
-        if constexpr (EPI == EPI_QKROPE || EPI == EPI_VSTORE) pos = p.ctl->pos;
+    if constexpr (EPI == EPI_QKROPE || EPI == EPI_VSTORE) pos = p.ctl->pos;
+    auto load_ep = [&](uint32_t ti) {
+        const uint32_t tile = min(gw + ti * stride, p.ntiles - 1);
 #pragma unroll
         for (int r = 0; r < RPL; ++r) {
-            const uint32_t row = min(tile_row(tile0, r), p.rows - 1);
-            pre_b[r] = 0.0f;
-            pre_r[r] = 0.0f;
+            const uint32_t row = min(tile_row(tile, r), p.rows - 1);
+            ep_b[r] = 0.0f;
+            ep_r[r] = 0.0f;
+            ep_y[r] = 0.0f;
             if constexpr (EPI == EPI_PLAIN) {
-                if (p.flags & F_BIAS) pre_b[r] = p.bias[row];
-                if (p.res) pre_r[r] = p.res[row];
+                if (p.flags & F_BIAS) ep_b[r] = p.bias[row];
+                if (p.res) ep_r[r] = p.res[row];
+                if (p.flags & F_ACCUM) ep_y[r] = p.y[row];
+            } else if constexpr (EPI == EPI_PARTIAL) {
+                if (p.flags & F_ACCUM) ep_y[r] = p.y[uint64_t(row) * p.nsplit + split];
             } else if constexpr (EPI == EPI_VSTORE) {
-                pre_b[r] = p.bias[row];
+                ep_b[r] = p.bias[row];
             } else if constexpr (EPI == EPI_QKROPE) {
-                pre_b[r] = row < p.row_split ? p.bias[row] : p.bias2[row - p.row_split];
+                ep_b[r] = row < p.row_split ? p.bias[row] : p.bias2[row - p.row_split];
             }
         }
         if constexpr (EPI == EPI_QKROPE) {
-            const uint32_t row = min(tile_row(tile0, 0), p.rows - 1);
+            const uint32_t row = min(tile_row(tile, 0), p.rows - 1);
             const uint32_t lr = row < p.row_split ? row : row - p.row_split;
-            pre_cs = p.rope[uint64_t(pos) * 64 + ((lr & 127u) >> 1)];
+            ep_cs = p.rope[uint64_t(pos) * 64 + ((lr & 127u) >> 1)];
         }
-    }
+    };
+    load_ep(0);
 
     if ((p.flags & F_NORM) && kb == 0 && nbl == p.nb) {
         stage_x_rms<FMT, NT>(lds, p.x, nbl, p.eps, p.normw, red);
@@ -759,17 +780,14 @@ __global__ __launch_bounds__(W * kWave) void k_gemv(GemvParams p)
             acc[n] = 0.0f;
         }
         if (v != 0 || bs != 0) return;
-        const bool first = ti == 0;
         if constexpr (EPI == EPI_QKROPE) {
             static_assert(RPL == 2, "RoPE pairs must sit in one lane");
             const uint32_t row = tile_row(tile, 0);  // even; row + 1 is its pair
             if (row >= p.rows) return;
             const bool isq = row < p.row_split;
             const uint32_t lr = isq ? row : row - p.row_split;
-            const float* bias = isq ? p.bias : p.bias2;
-            const float a = tot[0] + (first ? pre_b[0] : bias[lr]), b = tot[1] + (first ? pre_b[1] : bias[lr + 1]);
-            const float2 cs = first ? pre_cs : p.rope[uint64_t(pos) * 64 + ((lr & 127u) >> 1)];
-            const float c = cs.x, sv = cs.y;
+            const float a = tot[0] + ep_b[0], b = tot[1] + ep_b[1];
+            const float c = ep_cs.x, sv = ep_cs.y;
             const float ra = a * c - b * sv, rb = a * sv + b * c;
             if (isq) {
                 p.y[lr] = ra;
@@ -787,19 +805,19 @@ __global__ __launch_bounds__(W * kWave) void k_gemv(GemvParams p)
             if (row >= p.rows) continue;
             if constexpr (EPI == EPI_PLAIN) {
                 float val = tot[r];
-                if (p.flags & F_ACCUM) val = p.y[row] + val;
-                if (p.flags & F_BIAS) val = val + (first ? pre_b[r] : p.bias[row]);
-                if (p.res) val = (first ? pre_r[r] : p.res[row]) + val;
+                if (p.flags & F_ACCUM) val = ep_y[r] + val;
+                if (p.flags & F_BIAS) val = val + ep_b[r];
+                if (p.res) val = ep_r[r] + val;
                 p.y[row] = val;
             } else if constexpr (EPI == EPI_VSTORE) {
-                const float val = tot[r] + (first ? pre_b[r] : p.bias[row]);
+                const float val = tot[r] + ep_b[r];
                 p.cache[uint64_t(pos) * p.kv_dim + row] = _Float16(val);
             } else if constexpr (EPI == EPI_SWIGLU) {
                 const float g = tot[r], u = tot[RPL + r];
                 p.y[row] = (g / (1.0f + expf(-g))) * u;
             } else if constexpr (EPI == EPI_PARTIAL) {
                 float* dst = p.y + uint64_t(row) * p.nsplit + split;
-                *dst = (p.flags & F_ACCUM) ? *dst + tot[r] : tot[r];
+                *dst = (p.flags & F_ACCUM) ? ep_y[r] + tot[r] : tot[r];
             } else {
                 const float lv = tot[r];
                 if (p.y) p.y[row] = lv;
@@ -815,6 +833,8 @@ __global__ __launch_bounds__(W * kWave) void k_gemv(GemvParams p)
 
     uint32_t ci = 0, cj = 0;  // item being consumed
     auto step = [&](Blk (&next)[N], const Blk (&cur)[N]) {
+        if constexpr (EPI == EPI_PLAIN || EPI == EPI_PARTIAL || EPI == EPI_VSTORE || EPI == EPI_QKROPE)
+            if (cj == 0 && ci != 0) load_ep(ci);
         load_next(next);
         compute(cj, cur);
         if constexpr (EPI == EPI_COLPART)
@@ -938,6 +958,9 @@ inline int choose_waves(int epi, uint32_t /*rows*/, uint32_t blocks)
 inline Cfg choose_cfg(int epi, uint32_t rows, uint32_t blocks, uint32_t splits)
 {
     if (g_force.bs) return Cfg{g_force.bs, g_force.rpl, choose_waves(epi, rows, blocks)};
+    // fused gate/up: 4 quads per row (4 rows per wave tile) measured 5% faster
+    // than the 8 the balance score picks (Qwen2.5-7B shape, 17.8 vs 18.8 us)
+    if (epi == EPI_SWIGLU && blocks <= 16) return Cfg{4, 1, choose_waves(epi, rows, blocks)};
     static const Cfg cands[] = {{1, 1}, {1, 2}, {1, 4}, {2, 1}, {2, 2}, {2, 4}, {4, 1}, {4, 2}, {8, 1}, {8, 2}, {16, 1}};
     const double waves = 2048.0;
     Cfg best{1, 1};
