@@ -11,7 +11,8 @@ cannot serve them.
 value = algorithmic bytes per step (weights + x/s/y reads and writes,
 132,257,792 B) / time, in GB/s.  The roofline object is for the dominant
 kernel (the fused gate/up + SwiGLU launch), timed with HIP events on its
-own stream.  cpu_baseline times the oracle's serial-fp32 restatement of the
+own stream: K back-to-back launches over the same weight banks, median of
+three such loops after a warm-up.  cpu_baseline times the oracle's serial-fp32 restatement of the
 reference CPU kernels on the same workload (bounded sample, 1 thread).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -247,8 +248,11 @@ def main() -> int:
     arc.synchronize()
     gbs = BYTES_STEP / (ms / 1e3) / 1e9
 
-    time_loop(gateup, 10, stream)
-    ms_gu = time_loop(gateup, args.steps, stream)
+    # the roofline kernel back to back on its stream (launch latency hidden
+    # behind the previous launch, as in the step): warmed up until the clocks
+    # settle, then the median of three timed loops of K launches
+    time_loop(gateup, max(args.warmup, 50), stream)
+    ms_gu = sorted(time_loop(gateup, args.steps, stream) for _ in range(3))[1]
     ms_dn = time_loop(down, args.steps, stream)
     ach = BYTES_GATEUP / (ms_gu / 1e3) / 1e9
     log(f"step {ms * 1e3:.2f} us ({gbs:.1f} GB/s); gate/up {ms_gu * 1e3:.2f} us ({ach:.1f} GB/s); "
