@@ -414,7 +414,7 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         p.rope = S->rope;
         p.ctl = S->ctl;
         p.y = S->q;
-        if ((rc = chk(launch_one<kFmtQ4, EPI_QKROPE, 16, 2>(p, 1, st, nullptr), "q/k projection"))) return rc;
+        if ((rc = chk(launch_one<kFmtQ4, EPI_QKROPE, 16, 2, 8>(p, 1, st, nullptr), "q/k projection"))) return rc;
 
         // v projection + V store
         p = make_params(L.v_type, L.v, nullptr, KVD, H, S->h);
