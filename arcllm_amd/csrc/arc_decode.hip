@@ -1,11 +1,11 @@
 // arc_decode.hip -- the single-token greedy decode step of a Qwen2.5-shaped
 // model on gfx950, and its model/session C ABI (include/arcllm_hip.h).
 //
-// One decode step (src/arcllm_v1_runtime.cpp:371-421 restated as 7 launches
+// One decode step (src/arcllm_v1_runtime.cpp:371-421 restated as 6 launches
 // per layer instead of 16 dispatches):
 //   embed      token row of token_embd (Q4_K) -> h                      k_embed_q4k
-//   per layer  [attn RMSNorm + q/k GEMV + bias + RoPE + k -> fp16 cache] k_gemv<Q4,EPI_QKROPE>
-//              [attn RMSNorm + v GEMV + bias -> fp16 cache]              k_gemv<v,EPI_VSTORE>
+//   per layer  [attn RMSNorm + q/k GEMV + bias + RoPE + k -> fp16 cache  k_qkv<v format>
+//               and v GEMV + bias -> fp16 cache, one launch]
 //              [cached GQA over chunks of 64 positions]                  k_attn_chunk
 //              [chunk merge in chunk order]                              k_attn_merge
 //              [o GEMV + residual]                                       k_gemv<Q4,EPI_PLAIN>
@@ -339,6 +339,47 @@ __global__ __launch_bounds__(1024) void k_decode_next(const ArgBest* __restrict_
 
 namespace arc {
 
+// q/k and v projections in one launch: workgroups [0, gqk) run the q/k GEMV
+// (bias, RoPE, K store), the others the v GEMV (bias, V store).  Both read
+// the same attention-normed x and stage it in their own format's layout; the
+// role is uniform per workgroup.  One launch instead of two saves the v
+// projection's whole fixed cost (x staging, first-load latency, launch),
+// which is most of its time: its weights are 1.5 MB.
+template <int VFMT>
+__global__ __launch_bounds__(8 * kWave) void k_qkv(GemvParams qk, GemvParams v, uint32_t gqk)
+{
+    if (blockIdx.x < gqk)
+        gemv_body<kFmtQ4, 16, 2, EPI_QKROPE, 8>(qk, blockIdx.x, gqk);
+    else
+        gemv_body<VFMT, 16, 1, EPI_VSTORE, 8>(v, blockIdx.x - gqk, gridDim.x - gqk);
+}
+
+template <int VFMT>
+static hipError_t launch_qkv(GemvParams qk, GemvParams v, hipStream_t st)
+{
+    const Cfg cqk{16, 2, 8}, cv{16, 1, 8};
+    qk.ntiles = (qk.rows + tile_rows(cqk) - 1) / tile_rows(cqk);
+    v.ntiles = (v.rows + tile_rows(cv) - 1) / tile_rows(cv);
+    const size_t lds = size_t(std::max(qk.panel, v.panel)) * kXBlk * sizeof(float);
+    static int per_cu = 0;  // resident workgroups per CU (the panel is the model's hidden size)
+    if (!per_cu) {
+        int nb = 0;
+        if (lds > 65536)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_qkv<VFMT>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_qkv<VFMT>, 8 * kWave, lds) != hipSuccess || nb < 1)
+            nb = 1;
+        per_cu = nb;
+    }
+    const uint64_t resident = uint64_t(per_cu) * cu_count();
+    // each part gets at most one wave tile per wave and at most the resident count
+    const uint32_t gqk = uint32_t(std::min<uint64_t>(resident, (qk.ntiles + 7) / 8));
+    const uint32_t gv = uint32_t(std::min<uint64_t>(resident, (v.ntiles + 7) / 8));
+    if (g_dry_run) return hipSuccess;
+    hipLaunchKernelGGL(k_qkv<VFMT>, dim3(gqk + gv), dim3(8 * kWave), lds, st, qk, v, gqk);
+    return hipGetLastError();
+}
+
 static uint64_t packed_bytes(int qtype, uint32_t rows, uint32_t K)
 {
     return uint64_t(rows) * (K / kQK) * (qtype == kFmtQ4 ? kQ4Bytes : kQ6Bytes);
@@ -414,20 +455,18 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         p.rope = S->rope;
         p.ctl = S->ctl;
         p.y = S->q;
-        if ((rc = chk(launch_one<kFmtQ4, EPI_QKROPE, 16, 2, 8>(p, 1, st, nullptr), "q/k projection"))) return rc;
 
-        // v projection + V store
-        p = make_params(L.v_type, L.v, nullptr, KVD, H, S->h);
-        p.flags = F_NORM;
-        p.normw = L.attn_norm;
-        p.eps = d.rms_eps;
-        p.bias = L.vb;
-        p.kv_dim = KVD;
-        p.cache = vc;
-        p.ctl = S->ctl;
-        hipError_t e = L.v_type == kFmtQ4 ? launch_one<kFmtQ4, EPI_VSTORE, 16, 1>(p, 1, st, nullptr)
-                                          : launch_one<kFmtQ6, EPI_VSTORE, 16, 1>(p, 1, st, nullptr);
-        if ((rc = chk(e, "v projection"))) return rc;
+        // v projection + V store, in the same launch
+        GemvParams pv = make_params(L.v_type, L.v, nullptr, KVD, H, S->h);
+        pv.flags = F_NORM;
+        pv.normw = L.attn_norm;
+        pv.eps = d.rms_eps;
+        pv.bias = L.vb;
+        pv.kv_dim = KVD;
+        pv.cache = vc;
+        pv.ctl = S->ctl;
+        hipError_t e = L.v_type == kFmtQ4 ? launch_qkv<kFmtQ4>(p, pv, st) : launch_qkv<kFmtQ6>(p, pv, st);
+        if ((rc = chk(e, "q/k/v projection"))) return rc;
 
         // attention
         AttnParams ap{};

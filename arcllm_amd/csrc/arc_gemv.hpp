@@ -611,8 +611,11 @@ __device__ void wg_argmax(float bv, uint32_t bi, uint32_t nf, ArgBest* out)
 }
 
 // --------------------------------------------------------------- GEMV core
+// One workgroup's share of a GEMV launch: workgroup bx of gx (x dimension)
+// and split blockIdx.y.  k_gemv runs it over the whole grid; a fused launch
+// can give disjoint workgroup ranges to different GEMVs.
 template <int FMT, int BS, int RPL, int EPI, int W>
-__global__ __launch_bounds__(W * kWave) void k_gemv(GemvParams p)
+__device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint32_t gx)
 {
     static_assert(W == 4 || W == 8, "4 or 8 waves per workgroup");
     constexpr int NT = W * kWave;
@@ -637,8 +640,8 @@ __global__ __launch_bounds__(W * kWave) void k_gemv(GemvParams p)
     const uint32_t nbl = min(p.panel, split_end - kb);
     const uint32_t nj = (nbl + BS - 1) / BS;  // block slots per tile, uniform over the wave
 
-    const uint32_t gw = blockIdx.x * W + wave;
-    const uint32_t stride = gridDim.x * W;
+    const uint32_t gw = bx * W + wave;
+    const uint32_t stride = gx * W;
     const uint32_t my_tiles = gw < p.ntiles ? (p.ntiles - gw + stride - 1) / stride : 0u;
     const uint32_t S = my_tiles * nj;
 
@@ -856,7 +859,13 @@ __global__ __launch_bounds__(W * kWave) void k_gemv(GemvParams p)
     }
     if (s < S) step(buf[1], buf[0]);
 
-    if constexpr (EPI == EPI_ARGMAX) wg_argmax(best_v, best_i, nonfinite, p.best + blockIdx.x);
+    if constexpr (EPI == EPI_ARGMAX) wg_argmax(best_v, best_i, nonfinite, p.best + bx);
+}
+
+template <int FMT, int BS, int RPL, int EPI, int W>
+__global__ __launch_bounds__(W * kWave) void k_gemv(GemvParams p)
+{
+    gemv_body<FMT, BS, RPL, EPI, W>(p, blockIdx.x, gridDim.x);
 }
 
 // --------------------------------------------------------------- launching

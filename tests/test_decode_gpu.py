@@ -127,5 +127,5 @@ def test_qwen7b_shape_greedy_tokens_identical(qwen7b, ctx, steps):
     d, T, model = qwen7b
     sess, gpu, nf, ref, second, margins, scale = run_pair(d, T, model, 4096 + 64, ctx, 1234, steps, 99 + ctx)
     assert nf == 0
-    assert sess.kernels_per_step == 3 + 7 * d.layers  # embed, 7 per layer, LM head, next-token
+    assert sess.kernels_per_step == 3 + 6 * d.layers  # embed, 6 per layer, LM head, next-token
     assert assert_tokens_match(gpu, ref, second, margins, scale) >= steps // 2
