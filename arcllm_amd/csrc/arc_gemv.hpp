@@ -41,7 +41,8 @@ constexpr int kMaxWaves = 8;  // larger workgroups share one staged x when LDS l
 
 // EPI_COLPART: split-K with one super-block column per split -- each quad's
 // own sum is the partial of (column, row), written without a cross-quad
-// reduction, so every column of a row is handled by one launch.
+// reduction, so every column of a row is handled by one launch; with y2 set
+// the owning wave also adds the row's partials in column order.
 // EPI_QKROPE: decode q/k projection -- rows [0, row_split) of w0 (q) then
 // rows of w1 (k), + bias, RoPE on adjacent row pairs (2m, 2m+1) of each
 // 128-wide head (RPL = 2 keeps a pair in one lane), q -> y (fp32), k -> fp16
@@ -84,6 +85,7 @@ struct GemvParams {
     _Float16* cache;          // QKROPE/VSTORE: this layer's cache, [ctx][kv_dim]
     const float2* rope;       // QKROPE: (cos, sin) of pos * theta^(-2p/128), [ctx][64]
     const DecodeCtl* ctl;     // QKROPE/VSTORE: current position
+    float* y2;                // COLPART over all of K: y2 = res + fixed-order sum of the row's partials
 };
 
 // ------------------------------------------------------------ block loads
@@ -746,10 +748,13 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
         const uint32_t bl = bs + BS * j;
         if (bl < nbl) blk_dot<FMT, N>(b, lds + bl * kXBlk + v * kSlot, v, acc);
     };
-    // EPI_COLPART: quad sums of a tile's columns are held in registers and
-    // stored once per tile (row-major partials, coalesced per slot).
-    constexpr int kMaxNj = (EPI == EPI_COLPART) ? (kPanel + BS - 1) / BS : 1;
-    float cp[RPL][kMaxNj];
+    // EPI_COLPART: each quad's column sum goes to the wave's rows in LDS
+    // (after the staged x, row stride = panel).  At a tile's last column the
+    // wave stores its rows' partials (row-major, consecutive lanes on
+    // consecutive columns) and, with y2 set (the panel is all of K), lane 0 of
+    // each row group adds the row's partials in column order, then res: the
+    // split-K second pass, done by the wave that owns the row.
+    float* colp = lds + p.panel * kXBlk + uint32_t(wave * kTileRows) * p.panel;
     auto finish_column = [&](uint32_t ti, uint32_t j) {
         float tot[N];
 #pragma unroll
@@ -757,22 +762,33 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
             tot[n] = group_sum<4>(acc[n]);
             acc[n] = 0.0f;
         }
+        const uint32_t c = bs + BS * j;
+        if (v == 0 && c < nbl)
 #pragma unroll
-        for (int k = 0; k < kMaxNj; ++k)
-            if (uint32_t(k) == j)
-#pragma unroll
-                for (int r = 0; r < RPL; ++r) cp[r][k] = tot[r];
-        if (j != nj - 1 || v != 0) return;
-        const uint32_t tile = gw + ti * stride;
+            for (int r = 0; r < RPL; ++r) colp[uint32_t(rg * RPL + r) * p.panel + c] = tot[r];
+        if (j != nj - 1) return;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const uint32_t tile = gw + ti * stride, li = uint32_t(lane) & (4u * BS - 1u);
 #pragma unroll
         for (int r = 0; r < RPL; ++r) {
             const uint32_t row = tile_row(tile, r);
             if (row >= p.rows) continue;
-            float* dst = p.y + uint64_t(row) * p.nsplit + kb + bs;
-#pragma unroll
-            for (int k = 0; k < kMaxNj; ++k)
-                if (uint32_t(k) < nj && bs + BS * uint32_t(k) < nbl) dst[BS * k] = cp[r][k];
+            const float* src = colp + uint32_t(rg * RPL + r) * p.panel;
+            float* dst = p.y + uint64_t(row) * p.nsplit + kb;
+            for (uint32_t cc = li; cc < nbl; cc += 4u * BS) dst[cc] = src[cc];
+            if (p.y2 && li == 0) {
+                float sum = 0.0f;
+                for (uint32_t cc = 0; cc < nbl; ++cc) sum += src[cc];
+                if (p.res) sum += p.res[row];
+                p.y2[row] = sum;
+            }
         }
+        // the next tile's column sums overwrite these rows
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
     auto finish = [&](uint32_t ti) {
         const uint32_t tile = gw + ti * stride;
@@ -892,10 +908,10 @@ static int cu_count()
 
 // Resident workgroups per CU for one kernel instance (cached), >= 1.
 template <int FMT, int EPI, int BS, int RPL, int W>
-int occupancy(size_t lds)
+int occupancy(size_t lds, uint32_t panel)
 {
     static int occ[kPanel + 1] = {};
-    const int slot = int(lds / (kXBlk * sizeof(float)));
+    const int slot = int(panel);
     if (!occ[slot]) {
         if (lds > 65536)
             (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<FMT, BS, RPL, EPI, W>),
@@ -917,8 +933,9 @@ hipError_t launch_one(GemvParams p, uint32_t splits, hipStream_t s, uint32_t* gr
 {
     const Cfg c{BS, RPL, W};
     p.ntiles = (p.rows + tile_rows(c) - 1) / tile_rows(c);
-    const size_t lds = size_t(p.panel) * kXBlk * sizeof(float);
-    const int per_cu = g_wg_per_cu > 0 ? g_wg_per_cu : occupancy<FMT, EPI, BS, RPL, W>(lds);
+    size_t lds = size_t(p.panel) * kXBlk * sizeof(float);
+    if constexpr (EPI == EPI_COLPART) lds += size_t(W) * tile_rows(c) * p.panel * sizeof(float);
+    const int per_cu = g_wg_per_cu > 0 ? g_wg_per_cu : occupancy<FMT, EPI, BS, RPL, W>(lds, p.panel);
     const uint64_t resident = uint64_t(per_cu) * cu_count();
     const uint64_t want = (p.ntiles + W - 1) / W;  // one wave tile per wave
     uint64_t gx = (resident + splits - 1) / splits;

@@ -10,27 +10,45 @@
 namespace arc {
 
 // Fixed-order second pass of the split-K GEMV: y[r] = ((p0 + p1) + ...) + res,
-// with the partials of row r contiguous at part[r*splits].  Up to 128
-// partials are fetched in one batch (all loads in flight), then added in order.
-__global__ __launch_bounds__(64) void k_splitk_reduce(const float* __restrict__ part, uint32_t rows,
+// with the partials of row r contiguous at part[r*splits].  A workgroup
+// covers 64 rows; per batch of up to 128 split columns its 256 threads read
+// the rows' partials (contiguous when one batch holds every split) with all
+// loads in flight, into LDS rows padded to 129 floats, and thread r then adds
+// row r's partials in order.
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, uint32_t rows,
                                                        uint32_t splits, const float* __restrict__ residual,
                                                        float* __restrict__ y)
 {
-    const uint32_t r = blockIdx.x * 64u + threadIdx.x;
-    if (r >= rows) return;
-    const float* p = part + uint64_t(r) * splits;
+    constexpr uint32_t kRows = 64, kCols = 128, kStride = kCols + 1, kPer = kRows * kCols / 256;
+    __shared__ float tile[kRows * kStride];
+    const uint32_t r0 = blockIdx.x * kRows, tid = threadIdx.x;
+    const uint32_t nr = min(kRows, rows - r0);
     float s = 0.0f;
-    for (uint32_t j0 = 0; j0 < splits; j0 += 128) {
-        const uint32_t n = min(128u, splits - j0);
-        float v[128];
+    for (uint32_t j0 = 0; j0 < splits; j0 += kCols) {
+        const uint32_t n = min(kCols, splits - j0), total = nr * n;
+        float v[kPer];
 #pragma unroll
-        for (int i = 0; i < 128; ++i) v[i] = uint32_t(i) < n ? p[j0 + i] : 0.0f;
+        for (uint32_t i = 0; i < kPer; ++i) {
+            const uint32_t e = tid + 256u * i;
+            const uint32_t rr = e / n, j = e - rr * n;
+            v[i] = e < total ? part[uint64_t(r0 + rr) * splits + j0 + j] : 0.0f;
+        }
+        __syncthreads();  // the previous batch has been added
 #pragma unroll
-        for (int i = 0; i < 128; ++i)
-            if (uint32_t(i) < n) s += v[i];
+        for (uint32_t i = 0; i < kPer; ++i) {
+            const uint32_t e = tid + 256u * i;
+            const uint32_t rr = e / n, j = e - rr * n;
+            if (e < total) tile[rr * kStride + j] = v[i];
+        }
+        __syncthreads();
+        if (tid < nr)
+            for (uint32_t j = 0; j < n; ++j) s += tile[tid * kStride + j];
     }
-    if (residual) s += residual[r];
-    y[r] = s;
+    if (tid < nr) {
+        const uint32_t r = r0 + tid;
+        if (residual) s += residual[r];
+        y[r] = s;
+    }
 }
 
 // Second stage of the LM-head argmax: one workgroup folds the per-workgroup
@@ -225,17 +243,20 @@ int arc_gemv_splitk(int qtype, const void* w, uint32_t rows, uint32_t K, uint32_
     p.nsplit = used;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (p.split_bps == 1 && nb <= uint32_t(kPanel)) {
-        // one column per split: all columns in one launch, partial per quad
+        // one column per split, all columns in one launch: the wave owning a
+        // row computes its partials (one per quad and column) and then adds
+        // them in column order, so both passes run in this launch
         p.split_bps = nb;
         p.panel = nb;
+        p.y2 = y;
+        p.res = residual;
         Cfg c = choose_cfg(EPI_PLAIN, rows, nb, 1);
-        if (c.bs < 8) c = Cfg{8, 1, c.waves};  // per-slot partials are held in registers: <= 10 slots
-        rc = check_hip(launch_gemv_epi(EPI_COLPART, qtype, c, p, 1, s), "split-K pass 1");
-    } else {
-        rc = run_paneled(EPI_PARTIAL, qtype, p, used, s, "split-K pass 1");
+        if (c.bs < 8 || c.rpl > 2) c = Cfg{8, 1, c.waves};  // <= 4 rows per wave tile in LDS
+        return check_hip(launch_gemv_epi(EPI_COLPART, qtype, c, p, 1, s), "split-K");
     }
+    rc = run_paneled(EPI_PARTIAL, qtype, p, used, s, "split-K pass 1");
     if (rc) return rc;
-    hipLaunchKernelGGL(k_splitk_reduce, dim3((rows + 63) / 64), dim3(64), 0, s, partials, rows, used, residual, y);
+    hipLaunchKernelGGL(k_splitk_reduce, dim3((rows + 63) / 64), dim3(256), 0, s, partials, rows, used, residual, y);
     return check_hip(hipGetLastError(), "split-K pass 2");
 }
 

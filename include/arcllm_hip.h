@@ -108,6 +108,10 @@ int arc_gateup_swiglu(int qtype, const void *w_gate, const void *w_up, uint32_t 
  * the partials of each row in order j = 0..used-1 (no atomics), and adds
  * residual[r] last when residual != NULL.  used = ceil((K/256)/bps) (splits
  * that would own no column are dropped).  partials holds splits*rows floats.
+ * With one column per split (bps = 1, K/256 <= 80) both passes run in one
+ * launch: the wave that computes a row's partials stores them and adds them
+ * in the same order; otherwise pass 2 is a second launch.  Results are
+ * identical either way.
  * Replaces the ffn_down dispatch and the Q4 down backend route
  * (src/arcllm_v1_runtime.cpp:405-413,
  *  src/arcllm_v1_q4_vulkan_backend_v4_runtime.h:347-386). */

@@ -178,7 +178,7 @@ def test_gateup_swiglu(rows, K):
 @pytest.mark.parametrize(
     "qtype,rows,K,splits",
     [(arc.Q6_K, 3584, 18944, 74), (arc.Q6_K, 100, 2560, 3), (arc.Q4_K, 512, 2560, 5), (arc.Q4_K, 3584, 18944, 74),
-     (arc.Q6_K, 33, 2304, 9)],
+     (arc.Q6_K, 33, 2304, 9), (arc.Q4_K, 70, 38400, 150)],
 )
 def test_splitk(qtype, rows, K, splits):
     w = packed(qtype, rows, K, 30)
