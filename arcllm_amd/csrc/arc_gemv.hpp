@@ -612,6 +612,24 @@ __device__ void wg_argmax(float bv, uint32_t bi, uint32_t nf, ArgBest* out)
     }
 }
 
+// Register buffers in a GEMV's prefetch ring (PF - 1 items in flight while
+// one is consumed).
+#ifndef ARC_PF_Q4
+#define ARC_PF_Q4 2
+#endif
+#ifndef ARC_PF_Q6
+#define ARC_PF_Q6 2
+#endif
+#ifndef ARC_PF_E148
+#define ARC_PF_E148 2
+#endif
+template <int FMT, int EPI>
+constexpr int ring_depth()
+{
+    return FMT == kFmtQ4 ? ARC_PF_Q4 : FMT == kFmtQ6 ? ARC_PF_Q6 : ARC_PF_E148;
+}
+static_assert(ARC_PF_Q4 >= 2 && ARC_PF_Q6 >= 2 && ARC_PF_E148 >= 2, "a ring holds at least two buffers");
+
 // --------------------------------------------------------------- GEMV core
 // One workgroup's share of a GEMV launch: workgroup bx of gx (x dimension)
 // and split blockIdx.y.  k_gemv runs it over the whole grid; a fused launch
@@ -621,7 +639,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
 {
     static_assert(W == 4 || W == 8, "4 or 8 waves per workgroup");
     constexpr int NT = W * kWave;
-    constexpr int PF = 2;  // register buffers in the prefetch ring
+    constexpr int PF = ring_depth<FMT, EPI>();  // register buffers in the prefetch ring
     extern __shared__ float lds[];
     __shared__ float red[W];
     constexpr int NMAT = (EPI == EPI_SWIGLU) ? 2 : 1;
@@ -867,13 +885,16 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
     // behind a per-item exit test, the compiler folded them into one item per
     // iteration with copies between the buffers, and copying a buffer just
     // loaded waited for its loads, losing the prefetch.
-    static_assert(PF == 2, "the ring is written out for two buffers");
+    // Item k consumes buffer k % PF and loads into (k + PF - 1) % PF; the
+    // unrolled indices are constants, so no buffer is ever copied.
     uint32_t s = 0;
     for (; s + PF <= S; s += PF) {
-        step(buf[1], buf[0]);
-        step(buf[0], buf[1]);
+#pragma unroll
+        for (int k = 0; k < PF; ++k) step(buf[(k + PF - 1) % PF], buf[k]);
     }
-    if (s < S) step(buf[1], buf[0]);
+#pragma unroll
+    for (int k = 0; k < PF - 1; ++k)
+        if (s + k < S) step(buf[(k + PF - 1) % PF], buf[k]);
 
     if constexpr (EPI == EPI_ARGMAX) wg_argmax(best_v, best_i, nonfinite, p.best + bx);
 }
@@ -948,13 +969,32 @@ hipError_t launch_one(GemvParams p, uint32_t splits, hipStream_t s, uint32_t* gr
     return hipGetLastError();
 }
 
-template <int FMT, int EPI>
-hipError_t launch_cfg(const Cfg& c, const GemvParams& p, uint32_t splits, hipStream_t s, uint32_t* gx)
+// Forced configuration for tuning sweeps (bs = 0: automatic; waves = 0: automatic).
+static thread_local Cfg g_force{0, 0, 0};
+static thread_local int g_force_waves = 0;
+
+// Q6_K layouts with 4 rows per lane (256 VGPRs plus spills into AGPRs) are
+// not built: the 2-quad one took a GPU memory fault once, with no cause found
+// in its source or its code.  An automatic choice of 4 rows per lane runs
+// with 2 on Q6_K; a forced one is refused.
+template <int FMT>
+constexpr bool layout_built(int rpl)
 {
+    return !(FMT == kFmtQ6 && rpl == 4);
+}
+
+template <int FMT, int EPI>
+hipError_t launch_cfg(Cfg c, const GemvParams& p, uint32_t splits, hipStream_t s, uint32_t* gx)
+{
+    if (!layout_built<FMT>(c.rpl)) {
+        if (g_force.bs) return hipErrorInvalidValue;
+        c.rpl = 2;
+    }
 #define ARC_CASE(B, R)                                                         \
-    if (c.bs == B && c.rpl == R)                                               \
-        return c.waves == 8 ? launch_one<FMT, EPI, B, R, 8>(p, splits, s, gx)  \
-                            : launch_one<FMT, EPI, B, R, 4>(p, splits, s, gx);
+    if constexpr (layout_built<FMT>(R))                                        \
+        if (c.bs == B && c.rpl == R)                                           \
+            return c.waves == 8 ? launch_one<FMT, EPI, B, R, 8>(p, splits, s, gx)  \
+                                : launch_one<FMT, EPI, B, R, 4>(p, splits, s, gx);
     ARC_CASE(1, 1) ARC_CASE(1, 2) ARC_CASE(1, 4)
     ARC_CASE(2, 1) ARC_CASE(2, 2) ARC_CASE(2, 4)
     ARC_CASE(4, 1) ARC_CASE(4, 2)
@@ -963,10 +1003,6 @@ hipError_t launch_cfg(const Cfg& c, const GemvParams& p, uint32_t splits, hipStr
 #undef ARC_CASE
     return hipErrorInvalidValue;
 }
-
-// Forced configuration for tuning sweeps (bs = 0: automatic; waves = 0: automatic).
-static thread_local Cfg g_force{0, 0, 0};
-static thread_local int g_force_waves = 0;
 
 // Waves per workgroup.  A staged panel wider than 37 super-blocks (> 40 KB
 // of LDS) caps residency at 2-3 workgroups per CU, so 8-wave workgroups
