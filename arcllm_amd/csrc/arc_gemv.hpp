@@ -1027,6 +1027,10 @@ inline Cfg choose_cfg(int epi, uint32_t rows, uint32_t blocks, uint32_t splits)
     // fused gate/up: 4 quads per row (4 rows per wave tile) measured 5% faster
     // than the 8 the balance score picks (Qwen2.5-7B shape, 17.8 vs 18.8 us)
     if (epi == EPI_SWIGLU && blocks <= 16) return Cfg{4, 1, choose_waves(epi, rows, blocks)};
+    // LM head + argmax: 2 quads per row, one row per lane measured fastest of
+    // every layout (Q6_K 152064 x 3584: 91.8 vs 99.6 us for the (2, 2) the
+    // balance score picks)
+    if (epi == EPI_ARGMAX && blocks <= 16) return Cfg{2, 1, choose_waves(epi, rows, blocks)};
     static const Cfg cands[] = {{1, 1}, {1, 2}, {1, 4}, {2, 1}, {2, 2}, {2, 4}, {4, 1}, {4, 2}, {8, 1}, {8, 2}, {16, 1}};
     const double waves = 2048.0;
     Cfg best{1, 1};
