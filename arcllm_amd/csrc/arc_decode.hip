@@ -345,19 +345,29 @@ namespace arc {
 // role is uniform per workgroup.  One launch instead of two saves the v
 // projection's whole fixed cost (x staging, first-load latency, launch),
 // which is most of its time: its weights are 1.5 MB.
+// Quads per q/k row (2 rows per lane: RoPE pairs) and per v row.  8 and 8
+// measured fastest in the decode step (7B shape, 564 tokens/s at T = 512;
+// 16 and 16, tuned when q/k and v were separate launches, 541; 8 and 16, 562;
+// 4 and 4, 546).
+#ifndef ARC_QK_BS
+#define ARC_QK_BS 8
+#endif
+#ifndef ARC_V_BS
+#define ARC_V_BS 8
+#endif
 template <int VFMT>
 __global__ __launch_bounds__(8 * kWave) void k_qkv(GemvParams qk, GemvParams v, uint32_t gqk)
 {
     if (blockIdx.x < gqk)
-        gemv_body<kFmtQ4, 16, 2, EPI_QKROPE, 8>(qk, blockIdx.x, gqk);
+        gemv_body<kFmtQ4, ARC_QK_BS, 2, EPI_QKROPE, 8>(qk, blockIdx.x, gqk);
     else
-        gemv_body<VFMT, 16, 1, EPI_VSTORE, 8>(v, blockIdx.x - gqk, gridDim.x - gqk);
+        gemv_body<VFMT, ARC_V_BS, 1, EPI_VSTORE, 8>(v, blockIdx.x - gqk, gridDim.x - gqk);
 }
 
 template <int VFMT>
 static hipError_t launch_qkv(GemvParams qk, GemvParams v, hipStream_t st)
 {
-    const Cfg cqk{16, 2, 8}, cv{16, 1, 8};
+    const Cfg cqk{ARC_QK_BS, 2, 8}, cv{ARC_V_BS, 1, 8};
     qk.ntiles = (qk.rows + tile_rows(cqk) - 1) / tile_rows(cqk);
     v.ntiles = (v.rows + tile_rows(cv) - 1) / tile_rows(cv);
     const size_t lds = size_t(std::max(qk.panel, v.panel)) * kXBlk * sizeof(float);
