@@ -611,35 +611,46 @@ __global__ __launch_bounds__(256) void k_pf_qkv_epi(const float* __restrict__ pa
     }
 }
 
-// H[m] += fixed-order split sum; with NORM also X[m] = fp16((H[m] * inv) *
-// w), inv = 1/sqrt(mean(H[m]^2) + eps), the next RMSNorm.  Grid M, one row
-// per workgroup of 1024 threads; thread t owns columns t + 1024*k (k < 20:
-// n <= 20480, the model limit on hidden), whose split partials are loaded
-// column-parallel ahead of the in-order sums.
-constexpr int kResCols = 20;
-template <bool NORM>
+// Fixed-order second pass of a split-K projection with the residual and
+// (NORM) the next RMSNorm: H[m][c] += sum_s part[s][m][c] (s in order), X[m] =
+// fp16((H[m] * inv) * w), inv = 1/sqrt(mean(H[m]^2) + eps).  Grid M, one row
+// per workgroup of 1024 threads; thread t owns columns t + 1024*k (k < KC,
+// n <= 1024*KC), and loads the partials of 8 splits at a time, all in flight,
+// before adding them in split order.
+constexpr int kResCols = 20;  // n <= 20480, the model limit on hidden
+template <bool NORM, int KC>
 __global__ __launch_bounds__(1024) void k_pf_res_norm(const float* __restrict__ part, uint32_t splits, uint32_t mpad,
                                                       uint32_t n, float* __restrict__ h, const float* __restrict__ w,
                                                       float eps, _Float16* __restrict__ x, uint32_t ldx)
 {
+    static_assert(KC >= 1 && KC <= kResCols, "columns per thread");
+    constexpr uint32_t kBatch = 8;
     __shared__ float red[16];
     const uint32_t m = blockIdx.x, t = threadIdx.x;
     float* r = h + uint64_t(m) * n;
     const float* pm = part + uint64_t(m) * n;
     const uint64_t sstride = uint64_t(mpad) * n;
-    float a[kResCols];
+    float a[KC];
 #pragma unroll
-    for (int k = 0; k < kResCols; ++k) a[k] = 0.0f;
-    for (uint32_t s = 0; s < splits; ++s) {
+    for (int k = 0; k < KC; ++k) a[k] = 0.0f;
+    for (uint32_t s0 = 0; s0 < splits; s0 += kBatch) {
+        float v[kBatch][KC];
 #pragma unroll
-        for (int k = 0; k < kResCols; ++k) {
-            const uint32_t c = t + 1024u * k;
-            if (c < n) a[k] += pm[s * sstride + c];
-        }
+        for (uint32_t u = 0; u < kBatch; ++u)
+#pragma unroll
+            for (int k = 0; k < KC; ++k) {
+                const uint32_t c = t + 1024u * k;
+                v[u][k] = (s0 + u < splits && c < n) ? pm[(s0 + u) * sstride + c] : 0.0f;
+            }
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u)
+#pragma unroll
+            for (int k = 0; k < KC; ++k)
+                if (s0 + u < splits) a[k] += v[u][k];
     }
     float ss = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kResCols; ++k) {
+    for (int k = 0; k < KC; ++k) {
         const uint32_t c = t + 1024u * k;
         if (c < n) {
             a[k] = r[c] + a[k];
@@ -652,11 +663,25 @@ __global__ __launch_bounds__(1024) void k_pf_res_norm(const float* __restrict__ 
         const float inv = 1.0f / sqrtf(ss / float(n) + eps);
         _Float16* o = x + uint64_t(m) * ldx;
 #pragma unroll
-        for (int k = 0; k < kResCols; ++k) {
+        for (int k = 0; k < KC; ++k) {
             const uint32_t c = t + 1024u * k;
             if (c < n) o[c] = _Float16((a[k] * inv) * w[c]);
         }
     }
+}
+
+template <bool NORM>
+void launch_res_norm(uint32_t M, hipStream_t st, const float* part, uint32_t splits, uint32_t mpad, uint32_t n,
+                     float* h, const float* w, float eps, _Float16* x, uint32_t ldx)
+{
+    const uint32_t kc = (n + 1023u) / 1024u;
+    if (kc <= 4)
+        hipLaunchKernelGGL((k_pf_res_norm<NORM, 4>), dim3(M), dim3(1024), 0, st, part, splits, mpad, n, h, w, eps, x, ldx);
+    else if (kc <= 8)
+        hipLaunchKernelGGL((k_pf_res_norm<NORM, 8>), dim3(M), dim3(1024), 0, st, part, splits, mpad, n, h, w, eps, x, ldx);
+    else
+        hipLaunchKernelGGL((k_pf_res_norm<NORM, kResCols>), dim3(M), dim3(1024), 0, st, part, splits, mpad, n, h, w, eps,
+                           x, ldx);
 }
 
 // Causal GQA for query row m (position pos0 + m) and kv head g: the HPK q
@@ -1016,8 +1041,7 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             split_plan(g.N, g.nb, gx, sp, bps);
             g.bps = bps;
             if ((rc = chk(launch_gemm_mb<kFmtQ4, 1, false>(g, mb, gx, sp, st), "o projection"))) return rc;
-            hipLaunchKernelGGL(k_pf_res_norm<true>, dim3(M), dim3(1024), 0, st, pf->part, sp, uint32_t(kPfMaxM), H,
-                               pf->h, L.ffn_norm, d.rms_eps, pf->x, H);
+            launch_res_norm<true>(M, st, pf->part, sp, uint32_t(kPfMaxM), H, pf->h, L.ffn_norm, d.rms_eps, pf->x, H);
             if ((rc = chk(hipGetLastError(), "o residual + ffn norm"))) return rc;
             // gate/up + SwiGLU -> xs
             PfGemm u = g;
@@ -1047,11 +1071,10 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
                      "down projection");
             if (rc) return rc;
             if (l + 1 < d.layers) {
-                hipLaunchKernelGGL(k_pf_res_norm<true>, dim3(M), dim3(1024), 0, st, pf->part, sp, uint32_t(kPfMaxM), H,
-                                   pf->h, Mdl->layers[l + 1].attn_norm, d.rms_eps, pf->x, H);
+                launch_res_norm<true>(M, st, pf->part, sp, uint32_t(kPfMaxM), H, pf->h, Mdl->layers[l + 1].attn_norm,
+                                      d.rms_eps, pf->x, H);
             } else {
-                hipLaunchKernelGGL(k_pf_res_norm<false>, dim3(M), dim3(1024), 0, st, pf->part, sp, uint32_t(kPfMaxM),
-                                   H, pf->h, nullptr, 0.0f, nullptr, 0u);
+                launch_res_norm<false>(M, st, pf->part, sp, uint32_t(kPfMaxM), H, pf->h, nullptr, 0.0f, nullptr, 0u);
             }
             if ((rc = chk(hipGetLastError(), "down residual"))) return rc;
         }
