@@ -582,10 +582,18 @@ __global__ __launch_bounds__(256) void k_pf_qkv_epi(const float* __restrict__ pa
     const uint32_t c = 2 * (blockIdx.x * 256 + threadIdx.x);
     if (c >= N) return;
     float a = 0.0f, b = 0.0f;
-    for (uint32_t s = 0; s < splits; ++s) {
-        const float2 v = *reinterpret_cast<const float2*>(part + (uint64_t(s) * mpad + m) * N + c);
-        a += v.x;
-        b += v.y;
+    for (uint32_t s0 = 0; s0 < splits; s0 += 8) {  // 8 splits' loads in flight, added in split order
+        float2 v[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u)
+            v[u] = s0 + u < splits ? *reinterpret_cast<const float2*>(part + (uint64_t(s0 + u) * mpad + m) * N + c)
+                                   : float2{0.0f, 0.0f};
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u)
+            if (s0 + u < splits) {
+                a += v[u].x;
+                b += v[u].y;
+            }
     }
     if (c >= hidden + kv_dim) {
         const uint32_t lc = c - hidden - kv_dim;
@@ -715,15 +723,27 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ q, co
     __syncthreads();
     for (uint32_t t0 = 0; t0 < T; t0 += kChunk) {
         const uint32_t nt = min(uint32_t(kChunk), T - t0);
+        // every K and V load of the chunk is issued here, so the chunk costs
+        // one memory round trip
+        uint4 kraw[4];
+        half2_t vraw[16];
+        {
+            const uint4* kp = reinterpret_cast<const uint4*>(kc + uint64_t(t0 + min(tk, nt - 1)) * kvd + g * kHeadDim +
+                                                             part * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kraw[i] = kp[i];
+            const _Float16* vb = vc + uint64_t(t0) * kvd + g * kHeadDim + 2 * vi;
+#pragma unroll
+            for (int tt = 0; tt < 16; ++tt)
+                vraw[tt] = *reinterpret_cast<const half2_t*>(vb + uint64_t(min(uint32_t(pg * 16 + tt), nt - 1)) * kvd);
+        }
         {   // scores of positions t0 + tk
             float s[HPK];
 #pragma unroll
             for (int h = 0; h < HPK; ++h) s[h] = 0.0f;
-            const uint4* kp = reinterpret_cast<const uint4*>(kc + uint64_t(t0 + min(tk, nt - 1)) * kvd + g * kHeadDim +
-                                                             part * 32);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint4 raw = kp[i];
+                const uint4 raw = kraw[i];
                 const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
@@ -764,12 +784,11 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ q, co
                 o[h][0] *= alpha[h];
                 o[h][1] *= alpha[h];
             }
-            const _Float16* vb = vc + uint64_t(t0) * kvd + g * kHeadDim + 2 * vi;
-#pragma unroll 4
+#pragma unroll
             for (int tt = 0; tt < 16; ++tt) {
                 const uint32_t t = pg * 16 + tt;
                 const bool in = t < nt;
-                const half2_t vv = *reinterpret_cast<const half2_t*>(vb + uint64_t(min(t, nt - 1)) * kvd);
+                const half2_t vv = vraw[tt];
                 const float v0 = in ? static_cast<float>(vv.x) : 0.0f, v1 = in ? static_cast<float>(vv.y) : 0.0f;
 #pragma unroll
                 for (int h = 0; h < HPK; ++h) {
