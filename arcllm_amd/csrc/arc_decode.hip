@@ -228,6 +228,14 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnParams a)
     __shared__ float wred[2][4];
     __shared__ float4 ored[8][kHeadDim / 4];
 
+    // the first batch of chunk partials o (chunks j, j+8, .., j+56) is loaded
+    // before the m/l reduction, which it does not depend on
+    const uint32_t j = uint32_t(tid) >> 5, d4 = tid & 31;
+    const float4* src = reinterpret_cast<const float4*>(a.po + (uint64_t(g) * a.max_chunks * a.hpk + hl) * kHeadDim) + d4;
+    const uint32_t stride = a.hpk * (kHeadDim / 4);  // float4s between chunks
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[uint64_t(min(j + 8 * u, n - 1)) * stride];
     const float* pml = a.pml + (uint64_t(g) * a.max_chunks * a.hpk + hl) * 2;  // chunk c at + c*hpk*2
     float mv[kMaxChunks / 256], lv[kMaxChunks / 256];
     float M = -INFINITY;
@@ -261,14 +269,11 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnParams a)
     __syncthreads();
     L = ((wred[1][0] + wred[1][1]) + wred[1][2]) + wred[1][3];
 
-    const uint32_t j = uint32_t(tid) >> 5, d4 = tid & 31;
-    const float4* src = reinterpret_cast<const float4*>(a.po + (uint64_t(g) * a.max_chunks * a.hpk + hl) * kHeadDim) + d4;
-    const uint32_t stride = a.hpk * (kHeadDim / 4);  // float4s between chunks
     float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (uint32_t c0 = j; c0 < n; c0 += 64) {
-        float4 v[8];
+        if (c0 != j)
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = src[uint64_t(min(c0 + 8 * u, n - 1)) * stride];
+            for (int u = 0; u < 8; ++u) v[u] = src[uint64_t(min(c0 + 8 * u, n - 1)) * stride];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const uint32_t c = c0 + 8 * u;
