@@ -123,6 +123,22 @@ def test_gemv_every_layout(qtype, bs, rpl):
     assert orc.rel_err(y.download(np.float32), orc.gemv_r64(qtype, w, rows, K, x)) <= TOL
 
 
+def test_q6_four_rows_per_lane_layout_refused():
+    """Q6_K layouts with 4 rows per lane are not built: a forced one is
+    refused on the host (nothing is launched); the automatic choice never
+    takes it."""
+    rows, K = 64, 512
+    w = dev(packed(arc.Q6_K, rows, K, 9))
+    x = dev(arc.synth_normal(SEED, 10, K))
+    y = arc.DeviceBuffer(rows * 4)
+    arc.tune_force(2, 4)
+    try:
+        with pytest.raises(arc.ArcError):
+            arc.gemv(arc.Q6_K, w, rows, K, x, y)
+    finally:
+        arc.tune_force(0, 0)
+
+
 def test_gemv_q6_unaligned_base():
     """Q6_K tensor starting 2 bytes past a 4-byte boundary, odd blocks per row."""
     rows, K = 7, 768
