@@ -376,17 +376,18 @@ static hipError_t launch_qkv(GemvParams qk, GemvParams v, hipStream_t st)
     qk.ntiles = (qk.rows + tile_rows(cqk) - 1) / tile_rows(cqk);
     v.ntiles = (v.rows + tile_rows(cv) - 1) / tile_rows(cv);
     const size_t lds = size_t(std::max(qk.panel, v.panel)) * kXBlk * sizeof(float);
-    static int per_cu = 0;  // resident workgroups per CU (the panel is the model's hidden size)
-    if (!per_cu) {
+    static int occ[kPanel + 1] = {};  // resident workgroups per CU, by panel (the hidden size in blocks)
+    const uint32_t slot = std::max(qk.panel, v.panel);
+    if (!occ[slot]) {
         int nb = 0;
         if (lds > 65536)
             (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_qkv<VFMT>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_qkv<VFMT>, 8 * kWave, lds) != hipSuccess || nb < 1)
             nb = 1;
-        per_cu = nb;
+        occ[slot] = nb;
     }
-    const uint64_t resident = uint64_t(per_cu) * cu_count();
+    const uint64_t resident = uint64_t(occ[slot]) * cu_count();
     // each part gets at most one wave tile per wave and at most the resident count
     const uint32_t gqk = uint32_t(std::min<uint64_t>(resident, (qk.ntiles + 7) / 8));
     const uint32_t gv = uint32_t(std::min<uint64_t>(resident, (v.ntiles + 7) / 8));
