@@ -731,6 +731,8 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
                 if (p.flags & F_BIAS) ep_b[r] = p.bias[row];
                 if (p.res) ep_r[r] = p.res[row];
                 if (p.flags & F_ACCUM) ep_y[r] = p.y[row];
+            } else if constexpr (EPI == EPI_COLPART) {
+                if (p.y2 && p.res) ep_r[r] = p.res[row];
             } else if constexpr (EPI == EPI_PARTIAL) {
                 if (p.flags & F_ACCUM) ep_y[r] = p.y[uint64_t(row) * p.nsplit + split];
             } else if constexpr (EPI == EPI_VSTORE) {
@@ -799,7 +801,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
             if (p.y2 && li == 0) {
                 float sum = 0.0f;
                 for (uint32_t cc = 0; cc < nbl; ++cc) sum += src[cc];
-                if (p.res) sum += p.res[row];
+                if (p.res) sum += ep_r[r];
                 p.y2[row] = sum;
             }
         }
@@ -870,7 +872,8 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
 
     uint32_t ci = 0, cj = 0;  // item being consumed
     auto step = [&](Blk (&next)[N], const Blk (&cur)[N]) {
-        if constexpr (EPI == EPI_PLAIN || EPI == EPI_PARTIAL || EPI == EPI_VSTORE || EPI == EPI_QKROPE)
+        if constexpr (EPI == EPI_PLAIN || EPI == EPI_PARTIAL || EPI == EPI_VSTORE || EPI == EPI_QKROPE ||
+                      EPI == EPI_COLPART)
             if (cj == 0 && ci != 0) load_ep(ci);
         load_next(next);
         compute(cj, cur);
