@@ -123,6 +123,41 @@ def test_gemv_every_layout(qtype, bs, rpl):
     assert orc.rel_err(y.download(np.float32), orc.gemv_r64(qtype, w, rows, K, x)) <= TOL
 
 
+@pytest.mark.parametrize("qtype,rows", [(arc.Q6_K, 1001), (arc.Q4_K, 301), (arc.Q6_K, 3)])
+def test_wide_gemv_cooperative_ragged(qtype, rows):
+    """K = 18944 (74 super-blocks: the cooperative workgroup kernel) with row
+    counts that leave the last workgroup's tiles partly or wholly past the
+    end, with bias."""
+    K = 18944
+    w = packed(qtype, rows, K, 80)
+    x = arc.synth_normal(SEED, 81, K)
+    b = arc.synth_normal(SEED, 82, rows)
+    y = arc.DeviceBuffer(rows * 4)
+    arc.gemv(qtype, dev(w), rows, K, dev(x), y, bias=dev(b))
+    assert orc.rel_err(y.download(np.float32), orc.gemv_r64(qtype, w, rows, K, x, b)) <= TOL
+
+
+def test_wide_splitk_cooperative_ragged():
+    """One-column split-K on the cooperative kernel with a ragged row count:
+    partials against the oracle, y the in-order sum of the partials + res."""
+    rows, K, splits = 1001, 18944, 74
+    w = packed(arc.Q4_K, rows, K, 83)
+    x = arc.synth_normal(SEED, 84, K)
+    res = arc.synth_normal(SEED, 85, rows)
+    part = arc.DeviceBuffer(splits * rows * 4)
+    y = arc.DeviceBuffer(rows * 4)
+    arc.gemv_splitk(arc.Q4_K, dev(w), rows, K, splits, dev(x), part, y, residual=dev(res))
+    gp = part.download(np.float32, splits * rows).reshape(rows, splits).T
+    rp = orc.splitk_r64(arc.Q4_K, w, rows, K, splits, x)
+    for j in range(splits):
+        assert orc.rel_err(gp[j], rp[j]) <= TOL
+    acc = np.zeros(rows, np.float32)
+    for j in range(splits):
+        acc = (acc + gp[j]).astype(np.float32)
+    acc = (acc + res).astype(np.float32)
+    assert np.array_equal(acc.view(np.uint32), y.download(np.float32).view(np.uint32))
+
+
 def test_q6_four_rows_per_lane_layout_refused():
     """Q6_K layouts with 4 rows per lane are not built: a forced one is
     refused on the host (nothing is launched); the automatic choice never
