@@ -9,11 +9,14 @@ copies of the weights (default 8, 1.06 GB) so the 256 MB Infinity Cache
 cannot serve them.
 
 value = algorithmic bytes per step (weights + x/s/y reads and writes,
-132,257,792 B) / time, in GB/s.  The roofline object is for the dominant
-kernel (the fused gate/up + SwiGLU launch), timed with HIP events on its
-own stream: K back-to-back launches over the same weight banks, median of
-three such loops after a warm-up.  cpu_baseline times the oracle's serial-fp32 restatement of the
-reference CPU kernels on the same workload (bounded sample, 1 thread).
+132,257,792 B) / time, in GB/s.  Both kernels of the step are timed alone with
+HIP events on their stream (K back-to-back launches over the weight banks,
+median of three loops after a warm-up); the roofline object is the longer of
+the two.  Config 0 (the gate GEMV) and config 2 (RMSNorm + LM head + argmax)
+are timed the same way, the 28-layer decode (config 3) and the 256-token
+prompt pass (config 4) on the 7B-shaped model.  cpu_baseline times the
+oracle's serial-fp32 restatement of the reference CPU kernels on the same FFN
+block (bounded sample; 1 thread, and every thread the box gives the process).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -44,6 +47,7 @@ W_GATE = FFN * Q4_ROW                      # 38,191,104
 W_DOWN = H * Q6_ROW_DOWN                   # 55,695,360
 BYTES_GATEUP = 2 * W_GATE + H * 4 + FFN * 4                  # weights + x read + s write
 BYTES_DOWN = W_DOWN + FFN * 4 + H * 4                         # weights + s read + y write
+# (split-K partials are implementation traffic, not algorithmic bytes)
 BYTES_STEP = 2 * W_GATE + W_DOWN + H * 4 + FFN * 4 * 2 + H * 4  # 132,257,792
 BYTES_GATE = W_GATE + H * 4 + FFN * 4                        # config: single gate GEMV
 W_LM = VOC * (H // 256) * 210
@@ -87,7 +91,10 @@ def cpu_baseline(sample_reps: int) -> dict:
 
     step(1)  # warmup
     t1 = sorted(step(1) for _ in range(sample_reps))[sample_reps // 2]
-    ncores = min(os.cpu_count() or 1, 16)
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    # every thread the box gives this process: its affinity set, capped by the
+    # OpenMP thread count the box sets (its CPU share)
+    ncores = max(1, min(nproc, int(os.environ.get("OMP_NUM_THREADS", nproc))))
     step(ncores)
     tn = sorted(step(ncores) for _ in range(sample_reps))[sample_reps // 2]
     return {
@@ -98,7 +105,8 @@ def cpu_baseline(sample_reps: int) -> dict:
         "sample": f"full FFN block (gate+up+SwiGLU+down), median of {sample_reps} after 1 warmup; "
                   f"oracle serial-fp32 per-element decode, gcc -O2 -ffp-contract=off",
         "ms_per_step": round(t1 * 1e3, 2),
-        "all_cores": {"cores": ncores, "value": round(BYTES_STEP / tn / 1e9, 4), "ms_per_step": round(tn * 1e3, 2)},
+        "all_cores": {"cores": ncores, "nproc": nproc, "value": round(BYTES_STEP / tn / 1e9, 4),
+                      "ms_per_step": round(tn * 1e3, 2)},
     }
 
 
@@ -107,18 +115,23 @@ def decode_leg(steps: int, warmup: int, graph: bool = True) -> dict:
     (Q4_K attn q/k/o, gate, up; Q6_K attn v, ffn down, output), fp16 KV cache
     pre-filled with N(0, 1) to each context, `steps` tokens per context timed
     wall-clock around one captured-graph decode call (one graph replay per
-    token, token IDs downloaded at the end).  Bytes per token = all weights
-    + the K and V rows read by attention (2 * layers * (ctx+i) * kv_dim * 2 B)."""
+    token, token IDs downloaded at the end).  Bytes per token = the weights
+    the step reads (every layer tensor, the LM head, the output norm and ONE
+    embedding row: the model bytes minus the embedding table plus one row)
+    + the K and V rows attention reads (positions 0..ctx+i, 28 layers, fp16)
+    + the K and V row written."""
     d = arc.qwen25_7b_dims()
     log("decode: generating the 7B-shaped model")
     model = arc.Model(d, seed=SEED)
-    wbytes = model.weight_bytes
     kvd = d.kv_heads * d.head_dim
+    emb_table = d.vocab * (d.hidden // 256) * 144
+    emb_row = (d.hidden // 256) * 144
+    wbytes = model.weight_bytes - emb_table + emb_row
     ctxs = (512, 2048, 4096)
     sess = arc.Session(model, max(ctxs) + max(steps, warmup, 1))
     out = {"model": "Qwen2.5-7B shape, 28 layers, Q4_K_M layout, random init",
            "launch": "captured graph, one replay per token" if graph else "kernel-by-kernel launches",
-           "weight_bytes": wbytes, "steps": steps, "kernels_per_step": None, "contexts": {}}
+           "weight_bytes_read_per_token": wbytes, "steps": steps, "kernels_per_step": None, "contexts": {}}
     for ctx in ctxs:
         sess.fill_kv(ctx, SEED + ctx)
         sess.decode(1234, ctx, max(warmup, 1), graph=graph)  # captures the step graph on first use
@@ -126,7 +139,7 @@ def decode_leg(steps: int, warmup: int, graph: bool = True) -> dict:
         t0 = time.perf_counter()
         toks, nf = sess.decode(1234, ctx, steps, graph=graph)
         dt = time.perf_counter() - t0
-        kv_bytes = sum(2 * d.layers * (ctx + i + 1) * kvd * 2 for i in range(steps))
+        kv_bytes = sum(2 * d.layers * (ctx + i + 2) * kvd * 2 for i in range(steps))  # reads + the write
         gbs = (wbytes * steps + kv_bytes) / dt / 1e9
         out["contexts"][str(ctx)] = {"tokens_per_s": round(steps / dt, 2), "ms_per_token": round(dt / steps * 1e3, 4),
                                      "GB/s": round(gbs, 1), "frac_of_peak_hbm": round(gbs / PEAK_HBM_GBS, 4),
@@ -171,12 +184,88 @@ def prefill_leg(model, d, reps: int = 5) -> dict:
     return out
 
 
-def load_traffic() -> dict | None:
-    p = os.path.join(ROOT, "profiles", "gateup_swiglu_ffn7b_traffic.json")
-    if os.path.exists(p):
-        with open(p) as f:
-            return json.load(f)
-    return None
+def load_traffic() -> dict:
+    """HBM bytes per launch of the FFN block's two kernels, from the committed
+    rocprofv3 PMC summary (FETCH_SIZE scaled by the copy-kernel calibration,
+    plus WRITE_SIZE)."""
+    p = os.path.join(ROOT, "profiles", "ffn7b_traffic.json")
+    if not os.path.exists(p):
+        return {}
+    with open(p) as f:
+        return json.load(f)
+
+
+def ceiling(nbytes: int, banks: int, stream: arc.Stream, iters: int) -> float:
+    """Streaming-read ceiling at `nbytes` per launch, rotating over `banks`
+    initialised buffers: arc_probe_read (one coalesced 16 B load per lane per
+    iteration) at 2048 / 4096 / 8192 workgroups, best of the three."""
+    n = nbytes // 4096 * 4096
+    bufs = [arc.DeviceBuffer(n) for _ in range(banks)]
+    for b in bufs:
+        arc.check(arc.lib().arc_memset(b.ptr, 1, n, stream.handle))
+    out = arc.DeviceBuffer(8192 * 256 * 4)
+    best = 0.0
+    for grid in (2048, 4096, 8192):
+        fn = lambda i: arc.probe_read(bufs[i % banks], n, out, grid, stream)  # noqa: E731
+        time_loop(fn, 10, stream)
+        ms = time_loop(fn, iters, stream)
+        best = max(best, n / (ms / 1e3) / 1e9)
+    for b in bufs:
+        b.close()
+    out.close()
+    return best
+
+
+def kernel_entry(name: str, nbytes: int, ms: float, traffic: dict) -> dict:
+    ach = nbytes / (ms / 1e3) / 1e9
+    t = traffic.get(name, {})
+    return {"kernel": t.get("kernel", name), "bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS,
+            "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": t.get("bytes_per_launch"),
+            "avg_launch_us": round(ms * 1e3, 3), "algorithmic_bytes_per_launch": nbytes}
+
+
+def components(banks: list, B: int, x, s, stream: arc.Stream, steps: int) -> dict:
+    """Config 0 (the Q4_K gate GEMV alone) and config 2 (output RMSNorm +
+    Q6_K LM head [152064 x 3584] + argmax), each over rotating weight copies
+    larger than the Infinity Cache, K launches back to back, median of three
+    loops after a warm-up."""
+    comp = {}
+
+    def gate(i: int) -> None:
+        arc.gemv(arc.Q4_K, banks[i % B][0], FFN, H, x, s, stream=stream)
+
+    time_loop(gate, 50, stream)
+    gate_ms = sorted(time_loop(gate, steps, stream) for _ in range(3))[1]
+    comp["config0_q4k_gate_gemv"] = {"workload": "Q4_K GEMV [18944x3584], x fp32 [3584] -> y fp32 [18944]",
+                                     "algorithmic_bytes": BYTES_GATE, "us": round(gate_ms * 1e3, 3),
+                                     "GB/s": round(BYTES_GATE / (gate_ms / 1e3) / 1e9, 1),
+                                     "frac_of_peak_hbm": round(BYTES_GATE / (gate_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4)}
+    log(f"config 0 gate GEMV {gate_ms * 1e3:.2f} us")
+    lm_h = arc.synth_packed(arc.Q6_K, SEED, 5, VOC, H)
+    lm = [arc.DeviceBuffer.from_array(lm_h)]
+    c = arc.DeviceBuffer(W_LM)
+    arc.check(arc.lib().arc_memcpy_dtod(c.ptr, lm[0].ptr, W_LM, stream.handle))
+    lm.append(c)
+    h = arc.DeviceBuffer.from_array(arc.synth_normal(SEED, 6, H))
+    nw = arc.DeviceBuffer.from_array(arc.synth_normal(SEED, 7, H, 1.0, 0.05))
+    ws = arc.DeviceBuffer(arc.lmhead_workspace_bytes(arc.Q6_K, VOC, H))
+    out = arc.DeviceBuffer(8)
+
+    def head(i: int) -> None:
+        arc.lmhead_argmax(arc.Q6_K, lm[i % 2], VOC, H, h, nw, 1e-6, None, ws, out, stream)
+
+    time_loop(head, 10, stream)
+    n = max(steps // 4, 10)
+    lm_ms = sorted(time_loop(head, n, stream) for _ in range(3))[1]
+    comp["config2_lmhead_argmax"] = {"workload": "RMSNorm + Q6_K LM head [152064x3584] + argmax (two launches)",
+                                     "algorithmic_bytes": BYTES_LM, "us": round(lm_ms * 1e3, 3),
+                                     "GB/s": round(BYTES_LM / (lm_ms / 1e3) / 1e9, 1),
+                                     "frac_of_peak_hbm": round(BYTES_LM / (lm_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+                                     "token": int(out.download(np.uint32)[0])}
+    log(f"config 2 LM head + argmax {lm_ms * 1e3:.2f} us")
+    for b in lm + [h, nw, ws, out]:
+        b.close()
+    return comp
 
 
 def main() -> int:
@@ -187,7 +276,7 @@ def main() -> int:
     ap.add_argument("--banks", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-reps", type=int, default=3)
-    ap.add_argument("--components", action="store_true", help="also time the gate GEMV and LM head")
+    ap.add_argument("--no-components", action="store_true", help="skip the config 0 / config 2 legs")
     ap.add_argument("--no-decode", action="store_true", help="skip the 28-layer decode leg")
     ap.add_argument("--decode-steps", type=int, default=64)
     ap.add_argument("--decode-eager", action="store_true",
@@ -248,29 +337,30 @@ def main() -> int:
     arc.synchronize()
     gbs = BYTES_STEP / (ms / 1e3) / 1e9
 
-    # the roofline kernel back to back on its stream (launch latency hidden
-    # behind the previous launch, as in the step): warmed up until the clocks
-    # settle, then the median of three timed loops of K launches
+    # each kernel of the step back to back on its stream (launch latency
+    # hidden behind the previous launch, as in the step): warmed up until the
+    # clocks settle, then the median of three timed loops of K launches
     time_loop(gateup, max(args.warmup, 50), stream)
     ms_gu = sorted(time_loop(gateup, args.steps, stream) for _ in range(3))[1]
-    ms_dn = time_loop(down, args.steps, stream)
-    ach = BYTES_GATEUP / (ms_gu / 1e3) / 1e9
-    log(f"step {ms * 1e3:.2f} us ({gbs:.1f} GB/s); gate/up {ms_gu * 1e3:.2f} us ({ach:.1f} GB/s); "
-        f"down {ms_dn * 1e3:.2f} us ({BYTES_DOWN / (ms_dn / 1e3) / 1e9:.1f} GB/s)")
-
-    # practical read ceiling of this box at the same byte counts, same rotation
-    probe_out = arc.DeviceBuffer(2048 * 256 * 4)
-    probe = [arc.DeviceBuffer(BYTES_STEP // 4096 * 4096) for _ in range(B)]
-    ms_c_step = time_loop(lambda i: arc.probe_read(probe[i % B], probe[i % B].nbytes, probe_out, 2048, stream),
-                          args.steps, stream)
-    ms_c_gu = time_loop(lambda i: arc.probe_read(probe[i % B], BYTES_GATEUP // 4096 * 4096, probe_out, 2048, stream),
-                        args.steps, stream)
-    del probe
-    ceil_step = (BYTES_STEP // 4096 * 4096) / (ms_c_step / 1e3) / 1e9
-    ceil_gu = (BYTES_GATEUP // 4096 * 4096) / (ms_c_gu / 1e3) / 1e9
-    log(f"stream-read ceiling: {ceil_step:.0f} GB/s at {BYTES_STEP} B, {ceil_gu:.0f} GB/s at {BYTES_GATEUP} B")
+    time_loop(down, max(args.warmup, 50), stream)
+    ms_dn = sorted(time_loop(down, args.steps, stream) for _ in range(3))[1]
+    log(f"step {ms * 1e3:.2f} us ({gbs:.1f} GB/s); gate/up {ms_gu * 1e3:.2f} us "
+        f"({BYTES_GATEUP / (ms_gu / 1e3) / 1e9:.1f} GB/s); down split-K {ms_dn * 1e3:.2f} us "
+        f"({BYTES_DOWN / (ms_dn / 1e3) / 1e9:.1f} GB/s)")
 
     traffic = load_traffic()
+    kernels = {"gateup_swiglu": kernel_entry("gateup_swiglu", BYTES_GATEUP, ms_gu, traffic),
+               "down_splitk": kernel_entry("down_splitk", BYTES_DOWN, ms_dn, traffic)}
+    dominant = "gateup_swiglu" if ms_gu >= ms_dn else "down_splitk"
+    roof = dict(kernels[dominant])
+    roof["role"] = f"{dominant}: the longest kernel of the timed step"
+
+    # practical read ceiling of this box at the same byte counts, same rotation
+    ceil_step = ceiling(BYTES_STEP, B, stream, args.steps)
+    ceil_dom = ceiling(roof["algorithmic_bytes_per_launch"], B, stream, args.steps)
+    log(f"stream-read ceiling: {ceil_step:.0f} GB/s at {BYTES_STEP} B, {ceil_dom:.0f} GB/s at "
+        f"{roof['algorithmic_bytes_per_launch']} B")
+
     result = {
         "metric": "Q4_K/Q6_K GEMV HBM GB/s (% of peak); 7B-shape decode tokens/s, 1 MI355X",
         "value": round(gbs, 2),
@@ -291,54 +381,25 @@ def main() -> int:
             "hidden": H, "ffn": FFN, "splits": SPLITS, "algorithmic_bytes_per_step": BYTES_STEP,
             "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         },
-        "roofline": {
-            "kernel": "k_gemv<Q4_K, swiglu> (fused gate/up + SwiGLU)",
-            "bound": "hbm",
-            "achieved": round(ach, 2),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(ach / PEAK_HBM_GBS, 4),
-            "traffic": traffic.get("bytes_per_launch") if traffic else None,
-            "avg_launch_us": round(ms_gu * 1e3, 3),
-            "algorithmic_bytes_per_launch": BYTES_GATEUP,
-        },
+        "roofline": roof,
+        "kernels": kernels,
         "stream_ceiling": {
-            "kernel": "arc_probe_read (coalesced 16 B/lane streaming read, same bank rotation)",
+            "kernel": "arc_probe_read (coalesced 16 B/lane streaming read of initialised buffers, same bank "
+                      "rotation, best of 2048/4096/8192 workgroups)",
             "GB/s_at_step_bytes": round(ceil_step, 1),
-            "GB/s_at_gateup_bytes": round(ceil_gu, 1),
+            "GB/s_at_roofline_kernel_bytes": round(ceil_dom, 1),
             "value_frac_of_ceiling": round(gbs / ceil_step, 4),
-            "roofline_frac_of_ceiling": round(ach / ceil_gu, 4),
+            "roofline_frac_of_ceiling": round(roof["achieved"] / ceil_dom, 4),
         },
         "device": f"{name} {gfx}",
     }
 
-    if args.components:
-        comp = {}
-        gate_ms = time_loop(lambda i: arc.gemv(arc.Q4_K, banks[i % B][0], FFN, H, x, s, stream=stream),
-                            args.steps, stream)
-        comp["q4k_gate_gemv"] = {"us": round(gate_ms * 1e3, 3), "GB/s": round(BYTES_GATE / (gate_ms / 1e3) / 1e9, 1)}
-        banks.clear()
-        arc.synchronize()
-        lm_h = arc.synth_packed(arc.Q6_K, SEED, 5, VOC, H)
-        lm = [arc.DeviceBuffer.from_array(lm_h)]
-        for _ in range(1):
-            c = arc.DeviceBuffer(W_LM)
-            arc.check(arc.lib().arc_memcpy_dtod(c.ptr, lm[0].ptr, W_LM, stream.handle))
-            lm.append(c)
-        h = arc.DeviceBuffer.from_array(arc.synth_normal(SEED, 6, H))
-        nw = arc.DeviceBuffer.from_array(arc.synth_normal(SEED, 7, H, 1.0, 0.05))
-        ws = arc.DeviceBuffer(arc.lmhead_workspace_bytes(arc.Q6_K, VOC, H))
-        out = arc.DeviceBuffer(8)
-        lm_ms = time_loop(lambda i: arc.lmhead_argmax(arc.Q6_K, lm[i % 2], VOC, H, h, nw, 1e-6, None, ws, out,
-                                                      stream), max(args.steps // 4, 10), stream)
-        comp["q6k_lmhead_argmax"] = {"us": round(lm_ms * 1e3, 3),
-                                     "GB/s": round(BYTES_LM / (lm_ms / 1e3) / 1e9, 1),
-                                     "token": int(out.download(np.uint32)[0])}
-        result["components"] = comp
+    if not args.no_components:
+        result["components"] = components(banks, B, x, s, stream, args.steps)
 
     if not args.no_decode:
         banks.clear()
-        for buf in (probe_out, x, s, part, y):
+        for buf in (x, s, part, y):
             buf.close()
         arc.synchronize()
         result["decode"] = decode_leg(args.decode_steps, 8, graph=not args.decode_eager)
