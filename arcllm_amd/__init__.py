@@ -79,6 +79,7 @@ _SIGS = {
     "arc_rmsnorm": [_P, _P, _U32, _F, _P, _P],
     "arc_lmhead_workspace_bytes": [C.c_int, _U32, _U32],
     "arc_lmhead_argmax": [C.c_int, _P, _U32, _U32, _P, _P, _F, _P, _P, _P, _P],
+    "arc_lmhead_argmax_noalloc": [C.c_int, _P, _U32, _U32, _P, _P, _F, _P, _P, _P],
     "arc_synth_packed": [C.c_int, _U64, _U64, _U32, _U32, _F, _F, _P],
     "arc_synth_normal": [_U64, _U64, C.c_size_t, _F, _F, _P],
     "arc_tune_force": [C.c_int, C.c_int],
@@ -371,6 +372,14 @@ def lmhead_argmax(qtype: int, w, rows: int, K: int, h, normw, eps: float, logits
                   stream: Optional[Stream] = None) -> None:
     check(lib().arc_lmhead_argmax(qtype, _ptr(w), rows, K, _ptr(h), _ptr(normw), eps, _ptr(logits),
                                   _ptr(workspace), _ptr(out), _sp(stream)))
+
+
+def lmhead_argmax_noalloc(qtype: int, w, rows: int, K: int, h, normw, eps: float, logits, out,
+                          stream: Optional[Stream] = None) -> None:
+    """arc_lmhead_argmax with its argmax partials in the library's static
+    device scratch (no workspace, no allocation)."""
+    check(lib().arc_lmhead_argmax_noalloc(qtype, _ptr(w), rows, K, _ptr(h), _ptr(normw), eps, _ptr(logits),
+                                          _ptr(out), _sp(stream)))
 
 
 def probe_read(buf, nbytes: int, out, grid: int = 2048, stream: Optional[Stream] = None) -> None:

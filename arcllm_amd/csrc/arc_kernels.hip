@@ -6,8 +6,42 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 namespace arc {
+
+// Argmax partials of arc_lmhead_argmax_noalloc: one ArgBest per workgroup of
+// its LM-head launch, in a file-scope device array instead of a workspace.
+// Each device holds its own copy at its own address; host code never passes
+// the array's name to a kernel, only the address hipGetSymbolAddress returns
+// for the current device (scratch_on_device).  Every workgroup of a launch
+// writes its entry and the second stage reads exactly those entries, so
+// nothing needs clearing between calls.
+constexpr uint32_t kNoAllocBest = 8192;  // 128 KB per device
+static __device__ __align__(256) ArgBest scratch[kNoAllocBest];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static ArgBest* g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current.
+static int scratch_on_device(ArgBest** out)
+{
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "current device");
+    if (rc) return rc;
+    if (dev < 0 || dev >= kMaxDevices) return set_error(ARC_ERR_UNSUPPORTED, "device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        if ((rc = check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "scratch address"))) return rc;
+        if (!ptr) return set_error(ARC_ERR_DEVICE, "no device address for the argmax scratch");
+        g_scratch_ptr[dev] = static_cast<ArgBest*>(ptr);
+    }
+    *out = g_scratch_ptr[dev];
+    return ARC_OK;
+}
 
 // Fixed-order second pass of the split-K GEMV: y[r] = ((p0 + p1) + ...) + res,
 // with the partials of row r contiguous at part[r*splits].  A workgroup
@@ -299,6 +333,43 @@ int arc_lmhead_argmax(int qtype, const void* w, uint32_t rows, uint32_t K, const
     rc = check_hip(launch_gemv_epi(EPI_ARGMAX, qtype, c, p, 1, s, &gx), "lm-head launch");
     if (rc) return rc;
     hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(1024), 0, s, p.best, gx, out);
+    return check_hip(hipGetLastError(), "argmax launch");
+}
+
+int arc_lmhead_argmax_noalloc(int qtype, const void* w, uint32_t rows, uint32_t K, const float* h,
+                              const float* normw, float eps, float* logits, uint32_t* out, arc_stream_t stream)
+{
+    if (qtype == kFmtE148) return set_error(ARC_ERR_UNSUPPORTED, "the LM head takes Q4_K or Q6_K");
+    int rc = check_shape(qtype, w, rows, K);
+    if (rc) return rc;
+    if ((rc = check_vec(h, "h"))) return rc;
+    if (normw && (rc = check_vec(normw, "normw"))) return rc;
+    if (!out) return set_error(ARC_ERR_INVALID_ARGUMENT, "null out");
+    if (K / kQK > uint32_t(kPanel)) return set_error(ARC_ERR_UNSUPPORTED, "LM head supports K <= %d", kPanel * kQK);
+    ArgBest* best = nullptr;
+    if ((rc = scratch_on_device(&best))) return rc;
+    GemvParams p = make_params(qtype, w, nullptr, rows, K, h);
+    p.flags = normw ? F_NORM : 0u;
+    p.normw = normw;
+    p.eps = eps;
+    p.y = logits;
+    p.best = best;
+    const Cfg c = choose_cfg(EPI_ARGMAX, rows, p.nb, 1);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // size the grid first (host-side only): its workgroups must fit the scratch
+    uint32_t gx = 0;
+    g_dry_run = true;
+    const hipError_t e = launch_gemv_epi(EPI_ARGMAX, qtype, c, p, 1, s, &gx);
+    g_dry_run = false;
+    if ((rc = check_hip(e, "lm-head sizing"))) return rc;
+    if (gx > kNoAllocBest)
+        return set_error(ARC_ERR_UNSUPPORTED, "LM-head launch needs %u workgroup results, the scratch holds %u", gx,
+                         kNoAllocBest);
+    uint32_t gx2 = 0;
+    rc = check_hip(launch_gemv_epi(EPI_ARGMAX, qtype, c, p, 1, s, &gx2), "lm-head launch");
+    if (rc) return rc;
+    if (gx2 != gx) return set_error(ARC_ERR_DEVICE, "internal: LM-head grid changed (%u vs %u)", gx2, gx);
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(1024), 0, s, best, gx, out);
     return check_hip(hipGetLastError(), "argmax launch");
 }
 

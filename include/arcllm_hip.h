@@ -163,6 +163,21 @@ int arc_lmhead_argmax(int qtype, const void *w, uint32_t rows, uint32_t K, const
                       const float *normw, float eps, float *logits, void *workspace,
                       uint32_t *out, arc_stream_t stream);
 
+/* arc_lmhead_argmax without a workspace, for callers that cannot allocate
+ * device memory (code under stream/graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Same arguments, kernels and results as arc_lmhead_argmax; the per-workgroup
+ * argmax partials live in a static device array of 8192 entries (128 KB,
+ * held by each GPU the library runs on until the process ends).  Calls no
+ * allocator.  A launch that would need more than 8192 workgroup results is
+ * rejected with ARC_ERR_UNSUPPORTED (the grid never exceeds the resident
+ * workgroup count, at most 8192 on MI355X).  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (concurrent streams or threads)
+ * race and must be serialised by the caller. */
+int arc_lmhead_argmax_noalloc(int qtype, const void *w, uint32_t rows, uint32_t K, const float *h,
+                              const float *normw, float eps, float *logits, uint32_t *out,
+                              arc_stream_t stream);
+
 /* Tuning hook: force the GEMV lane layout for later launches on this host
  * thread (bs = super-block quads per row: 1,2,4,8,16; rpl = rows per lane:
  * 1,2,4).  bs = 0 restores the automatic choice. */
