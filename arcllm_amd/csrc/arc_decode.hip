@@ -1,24 +1,24 @@
 // arc_decode.hip -- the single-token greedy decode step of a Qwen2.5-shaped
 // model on gfx950, and its model/session C ABI (include/arcllm_hip.h).
 //
-// One decode step (src/arcllm_v1_runtime.cpp:371-421 restated as 6 launches
-// per layer instead of 16 dispatches):
-//   embed      token row of token_embd (Q4_K) -> h                      k_embed_q4k
+// One decode step (src/arcllm_v1_runtime.cpp:371-421 restated as 5 launches
+// per layer + 1 instead of 16 dispatches per layer + a host argmax):
 //   per layer  [attn RMSNorm + q/k GEMV + bias + RoPE + k -> fp16 cache  k_qkv<v format>
-//               and v GEMV + bias -> fp16 cache, one launch]
-//              [cached GQA over chunks of 64 positions]                  k_attn_chunk
-//              [chunk merge in chunk order]                              k_attn_merge
+//               and v GEMV + bias -> fp16 cache, one launch; layer 0
+//               decodes the token's embedding row while staging x]
+//              [cached GQA: chunk workgroups + last-arriver merge]       k_attn
 //              [o GEMV + residual]                                       k_gemv<Q4,EPI_PLAIN>
 //              [ffn RMSNorm + gate/up GEMV + SwiGLU]                     k_gemv<Q4,EPI_SWIGLU>
 //              [down GEMV + residual]                                    k_gemv<down,EPI_PLAIN>
-//   head       [output RMSNorm + LM head + argmax stage 1]               k_gemv<Q6,EPI_ARGMAX>
-//              [argmax stage 2 -> token, pos += 1]                       k_decode_next
+//   head       [output RMSNorm + LM head + argmax; the last workgroup
+//               picks the token and advances the control block]         k_gemv<Q6,EPI_ARGMAX>
 // The position and token live in a device control block, so the step is
 // captured once as a hipGraph and replayed per token.
 #include "arc_gemv.hpp"
 #include "arc_session.hpp"
 
 #include <cmath>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <memory>
@@ -28,317 +28,288 @@
 namespace arc {
 
 // ----------------------------------------------------------------- kernels
-// h = dequant(token_embd[token]) with the bit-exact element formula.
-__global__ __launch_bounds__(256) void k_embed_q4k(const uint8_t* __restrict__ emb, uint32_t nb,
-                                                   const DecodeCtl* __restrict__ ctl, float* __restrict__ h)
-{
-#pragma clang fp contract(off)
-    // workgroup b decodes super-block b of the row, one element per thread
-    const uint32_t token = ctl->token;
-    const uint8_t* row = emb + uint64_t(token) * nb * kQ4Bytes;
-    {
-        const uint32_t e = blockIdx.x * kQK + threadIdx.x;
-        const uint8_t* b = row + (e >> 8) * kQ4Bytes;
-        const uint32_t k = e & 255u, j = k >> 5;
-        const float d = f16_bits_to_f32(uint32_t(b[0]) | (uint32_t(b[1]) << 8));
-        const float dm = f16_bits_to_f32(uint32_t(b[2]) | (uint32_t(b[3]) << 8));
-        const uint8_t* s = b + 4;
-        uint32_t sc, mn;
-        if (j < 4) {
-            sc = s[j] & 63u;
-            mn = s[j + 4] & 63u;
-        } else {
-            sc = (s[j + 4] & 15u) | (uint32_t(s[j - 4] >> 6) << 4);
-            mn = (s[j + 4] >> 4) | (uint32_t(s[j] >> 6) << 4);
-        }
-        const uint32_t l64 = k & 63u;
-        const uint8_t qb = b[16 + (k >> 6) * 32 + (l64 & 31u)];
-        const uint32_t q = l64 < 32u ? (qb & 15u) : (qb >> 4);
-        const float t0 = d * float(sc);
-        const float t1 = t0 * float(q);
-        const float t2 = dm * float(mn);
-        h[e] = t1 - t2;
-    }
-}
-
 struct AttnParams {
     const float* q;           // [q_heads*128], RoPE applied
     const _Float16* kc;       // this layer's K cache [max_ctx][kv_heads*128]
     const _Float16* vc;       // this layer's V cache
     float* out;               // [q_heads*128]
-    float* po;                // chunk partials o: [kv_heads][max_chunks][hpk][128]
-    float* pml;               // chunk partials (m, l): [kv_heads][max_chunks][hpk][2]
+    float* po;                // split partials o: [kv_heads][kMaxSplits][hpk][128]
+    float* pml;               // split partials (m, l): [kv_heads][kMaxSplits][hpk][2]
+    uint32_t* counter;        // [kv_heads] arrival counters, zero between launches
     const DecodeCtl* ctl;
-    uint32_t kv_heads, hpk, max_chunks;
+    uint32_t kv_heads, hpk;
+    uint32_t max_ctx;         // cache rows per layer (loads are clamped to it)
     float scale;
 };
 
+// Split plan of one decode position over T cached positions: chunks of
+// kChunk positions, each split (workgroup) taking a run of cps consecutive
+// chunks in turn, at most kMaxSplits splits per kv head (one chunk per split
+// up to 2048 positions).  Measured on the 7B shape: one chunk per split with
+// the merge beats two chunks per split with half the merging (571 vs 551
+// tokens/s at 512 positions).
+struct AttnSplit {
+    uint32_t nch, cps, nsplit;
+};
+__device__ __host__ inline AttnSplit attn_split(uint32_t T)
+{
+    const uint32_t nch = (T + kChunk - 1) / kChunk;
+    const uint32_t cps = (nch + kMaxSplits - 1) / kMaxSplits;
+    return AttnSplit{nch, cps, (nch + cps - 1) / cps};
+}
 
-// Cached GQA for one new position, flash-decoding stage 1.  Workgroup (c, g)
-// covers positions [64c, 64c+64) of kv head g for its hpk query heads and
-// writes the chunk's softmax max m, sum l and weighted V sum o; every K and V
-// load is issued up front.  Stage 2 (k_attn_merge) combines the chunks; the
-// kernel boundary between the two makes the partials visible without
-// cross-workgroup fences.
+// LDS of k_attn (32-bit words): per stage K transposed as half2 pairs of
+// dims [64 dim pairs][kChunk + 1 pad] and V as [kChunk][64 dim pairs].
+constexpr int kKtStride = kChunk + 1;
+constexpr int kStageWords = (kHeadDim / 2) * kKtStride + kChunk * (kHeadDim / 2);
+constexpr int kAttnThreads = 512;  // 8 waves: wave w computes query head w of the group
+// The scores' softmax weights (one kChunk row per head wave), reused by the
+// merge for the split weights ([kMaxSplits][HPK]).
+template <int HPK>
+constexpr int attn_ew_words()
+{
+    constexpr int rows = HPK * kChunk, merge = kMaxSplits * HPK;
+    return rows > merge ? rows : merge;
+}
+
+// Cached GQA of one new position (flash decoding in one launch).  Workgroup
+// (s, g) covers the chunks of split s for kv head g; wave h computes query
+// head h of the group (lane = position for the scores, lane = dim pair for
+// the weighted V sum), so no reduction crosses waves.  Each chunk's K and V
+// are read once, coalesced, by all 512 threads and staged in LDS (K
+// transposed), double-buffered: the next chunk's loads are in flight while
+// one is used (the first chunk's are issued before the position is read:
+// its rows are clamped to the cache and masked later).  Per chunk and head:
+// scores, chunk softmax, weighted V sum, folded into the wave's running
+// (max, sum, o).  A single split writes the output; otherwise each split's
+// (m, l, o) goes to memory past the L2 (st_agent) and the last workgroup of
+// kv head g to arrive merges the splits in split order: M = max m_s,
+// f_s = e^(m_s - M), L = sum l_s f_s, out = sum o_s f_s / L.  Every
+// reduction has a fixed order, so the result does not depend on which
+// workgroup arrives last.
 // Semantics: src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1177-1212,
 // shaders/p7_attention_kv_online.comp (kv head = q head / (q_heads/kv_heads)).
 template <int HPK>
-__global__ __launch_bounds__(256) void k_attn_chunk(AttnParams a)
+__global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
 {
-    const uint32_t T = a.ctl->pos + 1;
-    const uint32_t nch = (T + kChunk - 1) / kChunk;
-    const uint32_t c = blockIdx.x, g = blockIdx.y;
-    if (c >= nch) return;
-    const uint32_t t0 = c * kChunk, nt = min(uint32_t(kChunk), T - t0);
-    constexpr uint32_t hpk = HPK;
+    extern __shared__ __align__(16) uint32_t smw[];
+    auto stage = [&](uint32_t i) { return smw + (i & 1u) * kStageWords; };
+    float* qs = reinterpret_cast<float*>(smw + 2 * kStageWords);  // [HPK][128]
+    float* ew = qs + HPK * kHeadDim;                               // [HPK waves][kChunk]; merge: [kMaxSplits][HPK]
+    float* mm = ew + attn_ew_words<HPK>();                          // [kMaxSplits][HPK] (+ [HPK])
+    float* ll = mm + kMaxSplits * HPK + HPK;                       // [kMaxSplits][HPK]
+    uint32_t* flag = reinterpret_cast<uint32_t*>(ll + kMaxSplits * HPK);
+
+    const uint32_t s = blockIdx.x, g = blockIdx.y;
     const uint32_t kvd = a.kv_heads * kHeadDim;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
 
-    __shared__ float qs[HPK][kHeadDim];
-    __shared__ float sc[HPK][kChunk];
-    __shared__ float ored[4][HPK][kHeadDim];
-    __shared__ float mh[HPK], lh[HPK];
+    // cooperative chunk load: 16 lanes per row, 16 B each (dims 8o .. 8o+7);
+    // thread t covers rows t/16 and t/16 + 32 of K and of V
+    const uint32_t lrow = uint32_t(tid) >> 4, oct = tid & 15;
+    const _Float16* kbase = a.kc + g * kHeadDim + 8 * oct;
+    const _Float16* vbase = a.vc + g * kHeadDim + 8 * oct;
+    uint4 rk0, rk1, rv0, rv1;
+#define ARC_ATTN_LOAD(t0, tmax)                                                                        \
+    do {                                                                                               \
+        const uint64_t r0 = min((t0) + lrow, (tmax)), r1 = min((t0) + lrow + 32u, (tmax));             \
+        rk0 = *reinterpret_cast<const uint4*>(kbase + r0 * kvd);                                       \
+        rv0 = *reinterpret_cast<const uint4*>(vbase + r0 * kvd);                                       \
+        rk1 = *reinterpret_cast<const uint4*>(kbase + r1 * kvd);                                       \
+        rv1 = *reinterpret_cast<const uint4*>(vbase + r1 * kvd);                                       \
+    } while (0)
+    // K words go to their dim-pair rows (transposed), V rows as read
+    auto put = [](uint32_t* st, uint32_t p, uint32_t o, const uint4& k, const uint4& v) {
+        st[(4 * o + 0) * kKtStride + p] = k.x;
+        st[(4 * o + 1) * kKtStride + p] = k.y;
+        st[(4 * o + 2) * kKtStride + p] = k.z;
+        st[(4 * o + 3) * kKtStride + p] = k.w;
+        *reinterpret_cast<uint4*>(st + (kHeadDim / 2) * kKtStride + p * (kHeadDim / 2) + 4 * o) = v;
+    };
 
-    // K: thread -> position tid/4, dims (tid%4)*32 .. +32 (4 x 16 B)
-    const uint32_t tk = uint32_t(tid) >> 2, part = tid & 3;
-    uint4 kraw[4];
-    {
-        const uint4* kp = reinterpret_cast<const uint4*>(a.kc + uint64_t(t0 + min(tk, nt - 1)) * kvd + g * kHeadDim +
-                                                         part * 32);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kraw[i] = kp[i];
-    }
-    // V: thread -> dims 2i, 2i+1 of positions 16*pg .. +16
-    const int vi = tid & 63, pg = tid >> 6;
-    half2_t vraw[16];
-    {
-        const _Float16* vb = a.vc + uint64_t(t0) * kvd + g * kHeadDim + 2 * vi;
-#pragma unroll
-        for (int tt = 0; tt < 16; ++tt)
-            vraw[tt] = *reinterpret_cast<const half2_t*>(vb + uint64_t(min(uint32_t(pg * 16 + tt), nt - 1)) * kvd);
-    }
-    for (uint32_t i = tid; i < hpk * kHeadDim; i += 256) qs[i >> 7][i & 127u] = a.q[g * hpk * kHeadDim + i];
+    ARC_ATTN_LOAD(s * kChunk, a.max_ctx - 1);  // chunk s: the first chunk of split s when cps = 1
+    for (uint32_t i = tid; i < HPK * kHeadDim; i += kAttnThreads) qs[i] = a.q[g * HPK * kHeadDim + i];
+
+    const uint32_t T = a.ctl->pos + 1;
+    const AttnSplit sp = attn_split(T);
+    if (s >= sp.nsplit) return;  // whole workgroup: not part of this position's plan
+    const uint32_t c0 = s * sp.cps, c1 = min(c0 + sp.cps, sp.nch);
+    if (sp.cps != 1) ARC_ATTN_LOAD(c0 * kChunk, T - 1);
+    put(stage(0), lrow, oct, rk0, rv0);
+    put(stage(0), lrow + 32u, oct, rk1, rv1);
     __syncthreads();
-    {   // scores
-        float s[HPK];
-#pragma unroll
-        for (int h = 0; h < HPK; ++h) s[h] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t w4[4] = {kraw[i].x, kraw[i].y, kraw[i].z, kraw[i].w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float kv = static_cast<float>(__builtin_bit_cast(half2_t, w4[e >> 1])[e & 1]);
-                const int d = part * 32 + i * 8 + e;
-#pragma unroll
-                for (int h = 0; h < HPK; ++h) s[h] = __builtin_fmaf(qs[h][d], kv, s[h]);
+
+    const int h = w;  // this wave's head (waves h >= HPK only load)
+    float o0 = 0.0f, o1 = 0.0f, M = -INFINITY, L = 0.0f;
+    for (uint32_t c = c0; c < c1; ++c) {
+        const uint32_t* st = stage(c - c0);
+        if (c + 1 < c1) ARC_ATTN_LOAD((c + 1) * kChunk, T - 1);
+        const uint32_t t0 = c * kChunk, nt = min(uint32_t(kChunk), T - t0);
+        if (h < HPK) {
+            // scores: lane = position, K consumed as fp16 (v_fma_mix)
+            const float* qh = qs + h * kHeadDim;
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four independent chains
+#pragma unroll 8
+            for (int dp = 0; dp < kHeadDim / 2; dp += 2) {
+                const float4 q4 = *reinterpret_cast<const float4*>(qh + 2 * dp);
+                const uint32_t k0 = st[dp * kKtStride + lane], k1 = st[(dp + 1) * kKtStride + lane];
+                acc[0] = fmix(k0, false, q4.x, acc[0]);
+                acc[1] = fmix(k0, true, q4.y, acc[1]);
+                acc[2] = fmix(k1, false, q4.z, acc[2]);
+                acc[3] = fmix(k1, true, q4.w, acc[3]);
             }
-        }
-#pragma unroll
-        for (int h = 0; h < HPK; ++h) s[h] = group_sum<4>(s[h]);
-        if (part == 0 && tk < nt)
-#pragma unroll
-            for (int h = 0; h < HPK; ++h)
-                sc[h][tk] = s[h] * a.scale;
-    }
-    __syncthreads();
-
-    {   // chunk softmax: wave w handles heads w and w+4
-        const int w = tid >> 6, lane = tid & 63;
-        for (uint32_t h = w; h < hpk; h += 4) {
-            const float s = uint32_t(lane) < nt ? sc[h][lane] : -INFINITY;
-            const float m = wave_max(s);
-            const float e = uint32_t(lane) < nt ? expf(s - m) : 0.0f;
+            const float sdot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+            const bool valid = uint32_t(lane) < nt;
+            const float x = valid ? sdot * a.scale : -INFINITY;
+            const float m = wave_max(x);
+            const float e = valid ? expf(x - m) : 0.0f;
             const float l = group_sum<kWave>(e);
-            sc[h][lane] = e;
-            if (lane == 0) {
-                mh[h] = m;
-                lh[h] = l;
+            ew[h * kChunk + lane] = e;  // read back by this wave only (in-order LDS)
+            // weighted V: lane = dim pair (2 lane, 2 lane + 1)
+            const uint32_t* vs = st + (kHeadDim / 2) * kKtStride;
+            float a0[2] = {0.0f, 0.0f}, a1[2] = {0.0f, 0.0f};  // even / odd positions
+#pragma unroll 4
+            for (int p = 0; p < kChunk; p += 4) {
+                const float4 e4 = *reinterpret_cast<const float4*>(ew + h * kChunk + p);
+                const float ee[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t v2 = vs[(p + u) * (kHeadDim / 2) + lane];
+                    a0[u & 1] = fmix(v2, false, ee[u], a0[u & 1]);
+                    a1[u & 1] = fmix(v2, true, ee[u], a1[u & 1]);
+                }
             }
+            const float Mn = fmaxf(M, m);
+            const float fo = expf(M - Mn), fc = expf(m - Mn);  // M = -inf first: fo = 0
+            o0 = o0 * fo + (a0[0] + a0[1]) * fc;
+            o1 = o1 * fo + (a1[0] + a1[1]) * fc;
+            L = L * fo + l * fc;
+            M = Mn;
         }
+        if (c + 1 < c1) {
+            put(stage(c + 1 - c0), lrow, oct, rk0, rv0);
+            put(stage(c + 1 - c0), lrow + 32u, oct, rk1, rv1);
+        }
+        __syncthreads();
+    }
+
+    float* out = a.out + uint64_t(g) * HPK * kHeadDim;
+    const uint64_t base = uint64_t(g) * kMaxSplits;
+    if (sp.nsplit == 1) {
+        if (h < HPK) {
+            const float li = 1.0f / L;
+            reinterpret_cast<float2*>(out + h * kHeadDim)[lane] = make_float2(o0 * li, o1 * li);
+        }
+        return;
+    }
+    // this split's partials, written past the L2 for the merging workgroup
+    if (h < HPK) {
+        float* po = a.po + ((base + s) * HPK + h) * kHeadDim + 2 * lane;
+        st_agent(po, o0);
+        st_agent(po + 1, o1);
+        if (lane == 0) {
+            st_agent(a.pml + ((base + s) * HPK + h) * 2, M);
+            st_agent(a.pml + ((base + s) * HPK + h) * 2 + 1, L);
+        }
+    }
+    if (!arrive_last(a.counter + g, sp.nsplit, flag)) return;
+
+    // merge (last workgroup of kv head g): thread -> (head hh, dims 2dp, 2dp+1);
+    // the splits' o in batches of 16, the first batch issued before the
+    // split weights are known
+    float* fw = ew;                      // [kMaxSplits][HPK] split weights (ew is free now)
+    float* Mh = mm + kMaxSplits * HPK;   // [HPK] (past mm; ll follows at its own offset)
+    const bool owner = uint32_t(tid) < HPK * (kHeadDim / 2);
+    const uint32_t hh = uint32_t(tid) / (kHeadDim / 2), dp = uint32_t(tid) % (kHeadDim / 2);
+    const float* src = a.po + (base * HPK + hh) * kHeadDim + 2 * dp;
+    constexpr int kB = 16;
+    float2 ov[kB];
+    if (owner)
+#pragma unroll
+        for (int u = 0; u < kB; ++u) ov[u] = ld_agent2(src + uint64_t(min(uint32_t(u), sp.nsplit - 1)) * HPK * kHeadDim);
+    if (uint32_t(tid) < sp.nsplit * HPK) {
+        const uint32_t ss = uint32_t(tid) / HPK, h2 = uint32_t(tid) - ss * HPK;
+        const float2 ml = ld_agent2(a.pml + ((base + ss) * HPK + h2) * 2);
+        mm[ss * HPK + h2] = ml.x;
+        ll[ss * HPK + h2] = ml.y;
     }
     __syncthreads();
-
-    {   // weighted V
-        float o[HPK][2];
-#pragma unroll
-        for (int h = 0; h < HPK; ++h) o[h][0] = o[h][1] = 0.0f;
-#pragma unroll
-        for (int tt = 0; tt < 16; ++tt) {
-            // positions past the chunk end carry p = 0 (softmax above) and a
-            // masked V, so the loop needs no branch
-            const uint32_t t = pg * 16 + tt;
-            const bool in = t < nt;
-            const float v0 = in ? static_cast<float>(vraw[tt].x) : 0.0f;
-            const float v1 = in ? static_cast<float>(vraw[tt].y) : 0.0f;
-#pragma unroll
-            for (int h = 0; h < HPK; ++h) {
-                const float p = sc[h][t];
-                o[h][0] = __builtin_fmaf(p, v0, o[h][0]);
-                o[h][1] = __builtin_fmaf(p, v1, o[h][1]);
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < HPK; ++h) {
-            ored[pg][h][2 * vi] = o[h][0];
-            ored[pg][h][2 * vi + 1] = o[h][1];
-        }
+    if (tid < HPK) {
+        float Mx = -INFINITY;
+        for (uint32_t ss = 0; ss < sp.nsplit; ++ss) Mx = fmaxf(Mx, mm[ss * HPK + tid]);
+        Mh[tid] = Mx;
     }
     __syncthreads();
+    if (uint32_t(tid) < sp.nsplit * HPK) fw[tid] = expf(mm[tid] - Mh[tid % HPK]);
+    __syncthreads();
+    if (tid < HPK) {
+        float Ls = 0.0f;
+        for (uint32_t ss = 0; ss < sp.nsplit; ++ss) Ls = __builtin_fmaf(ll[ss * HPK + tid], fw[ss * HPK + tid], Ls);
+        Mh[tid] = 1.0f / Ls;  // every thread has read Mh before the barrier above
+    }
+    if (owner) {
+        float r0 = 0.0f, r1 = 0.0f;
+        for (uint32_t s0 = 0; s0 < sp.nsplit; s0 += kB) {
+            if (s0 != 0)
+#pragma unroll
+                for (int u = 0; u < kB; ++u)
+                    ov[u] = ld_agent2(src + uint64_t(min(s0 + u, sp.nsplit - 1)) * HPK * kHeadDim);
+#pragma unroll
+            for (int u = 0; u < kB; ++u)
+                if (s0 + u < sp.nsplit) {
+                    const float f = fw[(s0 + u) * HPK + hh];
+                    r0 = __builtin_fmaf(ov[u].x, f, r0);
+                    r1 = __builtin_fmaf(ov[u].y, f, r1);
+                }
+        }
+        ov[0] = make_float2(r0, r1);
+    }
+    __syncthreads();
+    if (owner) {
+        const float li = Mh[hh];
+        reinterpret_cast<float2*>(out + hh * kHeadDim)[dp] = make_float2(ov[0].x * li, ov[0].y * li);
+    }
+#undef ARC_ATTN_LOAD
+}
 
-    const uint32_t phead = uint32_t(g) * a.max_chunks + c;
-    float* po = a.po + uint64_t(phead) * hpk * kHeadDim;
-    for (uint32_t idx = tid; idx < hpk * kHeadDim; idx += 256) {
-        const uint32_t h = idx >> 7, d = idx & 127u;
-        po[idx] = ((ored[0][h][d] + ored[1][h][d]) + ored[2][h][d]) + ored[3][h][d];
+template <int HPK>
+constexpr size_t attn_lds_bytes()
+{
+    return (size_t(2 * kStageWords) + HPK * kHeadDim + attn_ew_words<HPK>() + 2 * kMaxSplits * HPK + HPK + 4) * 4;
+}
+
+template <int HPK>
+static void launch_attn_hpk(const AttnParams& ap, dim3 grid, hipStream_t st)
+{
+    constexpr size_t lds = attn_lds_bytes<HPK>();
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn<HPK>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  int(lds));
+        attr = true;
     }
-    if (uint32_t(tid) < hpk) {
-        a.pml[(uint64_t(phead) * hpk + tid) * 2] = mh[tid];
-        a.pml[(uint64_t(phead) * hpk + tid) * 2 + 1] = lh[tid];
-    }
+    if (g_dry_run) return;
+    hipLaunchKernelGGL(k_attn<HPK>, grid, dim3(kAttnThreads), lds, st, ap);
 }
 
 // hpk is 1..kMaxHpk (checked with the model dims)
-static void launch_attn_chunk(const AttnParams& ap, dim3 grid, hipStream_t st)
+static void launch_attn(const AttnParams& ap, dim3 grid, hipStream_t st)
 {
     switch (ap.hpk) {
-    case 1: hipLaunchKernelGGL(k_attn_chunk<1>, grid, dim3(256), 0, st, ap); break;
-    case 2: hipLaunchKernelGGL(k_attn_chunk<2>, grid, dim3(256), 0, st, ap); break;
-    case 3: hipLaunchKernelGGL(k_attn_chunk<3>, grid, dim3(256), 0, st, ap); break;
-    case 4: hipLaunchKernelGGL(k_attn_chunk<4>, grid, dim3(256), 0, st, ap); break;
-    case 5: hipLaunchKernelGGL(k_attn_chunk<5>, grid, dim3(256), 0, st, ap); break;
-    case 6: hipLaunchKernelGGL(k_attn_chunk<6>, grid, dim3(256), 0, st, ap); break;
-    case 7: hipLaunchKernelGGL(k_attn_chunk<7>, grid, dim3(256), 0, st, ap); break;
-    default: hipLaunchKernelGGL(k_attn_chunk<8>, grid, dim3(256), 0, st, ap); break;
+    case 1: launch_attn_hpk<1>(ap, grid, st); break;
+    case 2: launch_attn_hpk<2>(ap, grid, st); break;
+    case 3: launch_attn_hpk<3>(ap, grid, st); break;
+    case 4: launch_attn_hpk<4>(ap, grid, st); break;
+    case 5: launch_attn_hpk<5>(ap, grid, st); break;
+    case 6: launch_attn_hpk<6>(ap, grid, st); break;
+    case 7: launch_attn_hpk<7>(ap, grid, st); break;
+    default: launch_attn_hpk<8>(ap, grid, st); break;
     }
 }
-static_assert(kMaxHpk == 8, "launch_attn_chunk instantiates 1..8");
-
-// Flash-decoding stage 2: workgroup h merges the chunks of query head h in
-// chunk order.  M = max m_c, f_c = e^(m_c - M), L = sum l_c f_c,
-// out = sum o_c f_c / L.  Thread (j, d4) accumulates dims 4*d4 .. +3 over
-// chunks j, j+8, ...; the eight lanes are then summed in order.
-__global__ __launch_bounds__(256) void k_attn_merge(AttnParams a)
-{
-    const uint32_t T = a.ctl->pos + 1;
-    const uint32_t n = (T + kChunk - 1) / kChunk;
-    const uint32_t hq = blockIdx.x, g = hq / a.hpk, hl = hq - g * a.hpk;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    __shared__ float ff[kMaxChunks];
-    __shared__ float wred[2][4];
-    __shared__ float4 ored[8][kHeadDim / 4];
-
-    // the first batch of chunk partials o (chunks j, j+8, .., j+56) is loaded
-    // before the m/l reduction, which it does not depend on
-    const uint32_t j = uint32_t(tid) >> 5, d4 = tid & 31;
-    const float4* src = reinterpret_cast<const float4*>(a.po + (uint64_t(g) * a.max_chunks * a.hpk + hl) * kHeadDim) + d4;
-    const uint32_t stride = a.hpk * (kHeadDim / 4);  // float4s between chunks
-    float4 v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = src[uint64_t(min(j + 8 * u, n - 1)) * stride];
-    const float* pml = a.pml + (uint64_t(g) * a.max_chunks * a.hpk + hl) * 2;  // chunk c at + c*hpk*2
-    float mv[kMaxChunks / 256], lv[kMaxChunks / 256];
-    float M = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < kMaxChunks / 256; ++r) {
-        const uint32_t c = uint32_t(r * 256 + tid);
-        mv[r] = -INFINITY;
-        lv[r] = 0.0f;
-        if (c < n) {
-            mv[r] = pml[uint64_t(c) * a.hpk * 2];
-            lv[r] = pml[uint64_t(c) * a.hpk * 2 + 1];
-        }
-        M = fmaxf(M, mv[r]);
-    }
-    M = wave_max(M);
-    if (lane == 0) wred[0][w] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3]));
-    float L = 0.0f;
-#pragma unroll
-    for (int r = 0; r < kMaxChunks / 256; ++r) {
-        const uint32_t c = uint32_t(r * 256 + tid);
-        if (c < n) {
-            const float f = expf(mv[r] - M);
-            ff[c] = f;
-            L = __builtin_fmaf(lv[r], f, L);
-        }
-    }
-    L = group_sum<kWave>(L);
-    if (lane == 0) wred[1][w] = L;
-    __syncthreads();
-    L = ((wred[1][0] + wred[1][1]) + wred[1][2]) + wred[1][3];
-
-    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t c0 = j; c0 < n; c0 += 64) {
-        if (c0 != j)
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = src[uint64_t(min(c0 + 8 * u, n - 1)) * stride];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const uint32_t c = c0 + 8 * u;
-            if (c < n) {
-                const float f = ff[c];
-                acc.x = __builtin_fmaf(v[u].x, f, acc.x);
-                acc.y = __builtin_fmaf(v[u].y, f, acc.y);
-                acc.z = __builtin_fmaf(v[u].z, f, acc.z);
-                acc.w = __builtin_fmaf(v[u].w, f, acc.w);
-            }
-        }
-    }
-    ored[j][d4] = acc;
-    __syncthreads();
-    if (tid < 32) {
-        float4 r = ored[0][tid];
-#pragma unroll
-        for (int k = 1; k < 8; ++k) {
-            r.x += ored[k][tid].x;
-            r.y += ored[k][tid].y;
-            r.z += ored[k][tid].z;
-            r.w += ored[k][tid].w;
-        }
-        const float inv = 1.0f / L;
-        reinterpret_cast<float4*>(a.out + uint64_t(hq) * kHeadDim)[tid] = {r.x * inv, r.y * inv, r.z * inv, r.w * inv};
-    }
-}
-
-// Argmax stage 2 of a decode step: token = argmax, recorded at out[step];
-// the control block advances to the next position.
-__global__ __launch_bounds__(1024) void k_decode_next(const ArgBest* __restrict__ best, uint32_t n,
-                                                      DecodeCtl* __restrict__ ctl, uint32_t* __restrict__ out,
-                                                      uint32_t out_cap)
-{
-    float bv = -INFINITY;
-    uint32_t bi = 0xffffffffu, nf = 0;
-    for (uint32_t i0 = 0; i0 < n; i0 += 4096u) {
-        ArgBest b[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t i = i0 + k * 1024u + threadIdx.x;
-            b[k] = i < n ? best[i] : ArgBest{-INFINITY, 0xffffffffu, 0u, 0u};
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if (b[k].idx != 0xffffffffu && arg_better(b[k].val, b[k].idx, bv, bi)) {
-                bv = b[k].val;
-                bi = b[k].idx;
-            }
-            nf += b[k].nonfinite;
-        }
-    }
-    __shared__ ArgBest res;
-    wg_argmax(bv, bi, nf, &res);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t tok = (res.idx == 0xffffffffu) ? 0u : res.idx;
-        const uint32_t step = ctl->step;
-        if (step < out_cap) out[step] = tok;
-        ctl->token = tok;
-        ctl->nonfinite += res.nonfinite;
-        ctl->step = step + 1;
-        ctl->pos += 1;
-    }
-}
+static_assert(kMaxHpk == 8, "launch_attn instantiates 1..8");
+static_assert(kMaxHpk <= kAttnThreads / kWave, "one wave per query head of a kv head");
+static_assert(kMaxHpk * (kHeadDim / 2) <= kAttnThreads && kMaxSplits * kMaxHpk <= kAttnThreads,
+              "merge: one thread per (head, dim pair) and per (split, head)");
 
 }  // namespace arc
 
@@ -404,7 +375,8 @@ static uint64_t packed_bytes(int qtype, uint32_t rows, uint32_t K)
 static int dims_ok(const arc_model_dims& d)
 {
     if (d.hidden == 0 || d.hidden % kQK || d.ffn == 0 || d.ffn % kQK || d.head_dim != kHeadDim || d.q_heads == 0 ||
-        d.kv_heads == 0 || d.q_heads % d.kv_heads || d.q_heads / d.kv_heads > kMaxHpk ||
+        d.kv_heads == 0 || d.kv_heads > uint32_t(kCounterLmHead - kCounterAttn) || d.q_heads % d.kv_heads ||
+        d.q_heads / d.kv_heads > kMaxHpk ||
         d.q_heads * kHeadDim != d.hidden || d.vocab == 0 || d.layers == 0 || d.layers > ARC_MAX_LAYERS)
         return set_error(ARC_ERR_UNSUPPORTED,
                          "unsupported model dims (hidden %u, heads %u/%u, head_dim %u, ffn %u, vocab %u, layers %u)",
@@ -417,29 +389,36 @@ static int dims_ok(const arc_model_dims& d)
     return ARC_OK;
 }
 
-// Launch one decode step on the session stream (captured into a graph by the
-// caller, or run eagerly).  Returns the number of kernels launched.
+// Output RMSNorm + LM head + argmax of the hidden row x in one launch: the
+// last workgroup to arrive picks the token and advances the control block.
 int launch_lm_head(arc_session* S, const float* x, bool logits, hipStream_t st)
 {
     const arc_model* M = S->model;
     const arc_model_dims& d = M->dims;
     const uint32_t H = d.hidden;
     GemvParams p = make_params(kFmtQ6, M->out, nullptr, d.vocab, H, x);
-    p.flags = F_NORM;
+    p.flags = F_NORM | F_ARGNEXT;
     p.normw = M->out_norm;
     p.eps = d.rms_eps;
     p.y = logits ? S->logits : nullptr;
     p.best = S->best;
+    p.counter = S->counters + kCounterLmHead;
+    p.ctl = S->ctl;
+    p.out_tokens = S->out_tokens;
+    p.out_cap = S->out_cap;
+    const Cfg c = choose_cfg(EPI_ARGMAX, d.vocab, H / kQK, 1);
     uint32_t gx = 0;
-    int rc = check_hip(launch_gemv_epi(EPI_ARGMAX, kFmtQ6, choose_cfg(EPI_ARGMAX, d.vocab, H / kQK, 1), p, 1, st, &gx),
-                       "lm head");
+    const bool dry = g_dry_run;
+    g_dry_run = true;  // size the grid first: every workgroup needs a partials slot
+    int rc = check_hip(launch_gemv_epi(EPI_ARGMAX, kFmtQ6, c, p, 1, st, &gx), "lm head");
+    g_dry_run = dry;
     if (rc) return rc;
     if (gx > S->best_cap) return set_error(ARC_ERR_UNSUPPORTED, "internal: argmax grid %u > %u", gx, S->best_cap);
-    if (!g_dry_run)
-        hipLaunchKernelGGL(k_decode_next, dim3(1), dim3(1024), 0, st, S->best, gx, S->ctl, S->out_tokens, S->out_cap);
-    return check_hip(hipGetLastError(), "argmax");
+    return check_hip(launch_gemv_epi(EPI_ARGMAX, kFmtQ6, c, p, 1, st, &gx), "lm head");
 }
 
+// Launch one decode step on the session stream (captured into a graph by the
+// caller, or run eagerly).  Returns the number of kernels launched.
 static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
 {
     arc_model* M = S->model;
@@ -447,18 +426,16 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
     hipStream_t st = S->stream;
     const uint32_t H = d.hidden, KVD = d.kv_heads * kHeadDim, F = d.ffn;
     uint32_t n = 0;
+    int rc = 0;
     auto chk = [&](hipError_t e, const char* what) { ++n; return check_hip(e, what); };
-
-    if (!g_dry_run) hipLaunchKernelGGL(k_embed_q4k, dim3(H / kQK), dim3(kQK), 0, st, M->emb, H / kQK, S->ctl, S->h);
-    int rc = chk(hipGetLastError(), "embed");
-    if (rc) return rc;
 
     for (uint32_t l = 0; l < d.layers; ++l) {
         const Layer& L = M->layers[l];
         _Float16* kc = S->kcache + uint64_t(l) * S->max_ctx * KVD;
         _Float16* vc = S->vcache + uint64_t(l) * S->max_ctx * KVD;
 
-        // q/k projection + RoPE + K store
+        // q/k projection + RoPE + K store; layer 0 decodes the token's
+        // embedding row as its x and writes it to h (the residual)
         GemvParams p = make_params(kFmtQ4, L.q, L.k, H + KVD, H, S->h);
         p.flags = F_NORM;
         p.normw = L.attn_norm;
@@ -481,6 +458,13 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         pv.kv_dim = KVD;
         pv.cache = vc;
         pv.ctl = S->ctl;
+        if (l == 0) {
+            p.flags |= F_EMBED;
+            p.emb = M->emb;
+            p.h_out = S->h;
+            pv.flags |= F_EMBED;
+            pv.emb = M->emb;
+        }
         hipError_t e = L.v_type == kFmtQ4 ? launch_qkv<kFmtQ4>(p, pv, st) : launch_qkv<kFmtQ6>(p, pv, st);
         if ((rc = chk(e, "q/k/v projection"))) return rc;
 
@@ -492,15 +476,14 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         ap.out = S->attn;
         ap.po = S->apo;
         ap.pml = S->apml;
+        ap.counter = S->counters + kCounterAttn;
         ap.ctl = S->ctl;
         ap.kv_heads = d.kv_heads;
         ap.hpk = d.q_heads / d.kv_heads;
-        ap.max_chunks = S->max_chunks;
+        ap.max_ctx = S->max_ctx;
         ap.scale = 1.0f / std::sqrt(float(kHeadDim));
-        if (!g_dry_run) launch_attn_chunk(ap, dim3(S->max_chunks, d.kv_heads), st);
-        if ((rc = chk(hipGetLastError(), "attention chunks"))) return rc;
-        if (!g_dry_run) hipLaunchKernelGGL(k_attn_merge, dim3(d.q_heads), dim3(256), 0, st, ap);
-        if ((rc = chk(hipGetLastError(), "attention merge"))) return rc;
+        launch_attn(ap, dim3(kMaxSplits, d.kv_heads), st);
+        if ((rc = chk(hipGetLastError(), "attention"))) return rc;
 
         // o projection + residual: h1 = h + Wo attn
         p = make_params(kFmtQ4, L.o, nullptr, H, H, S->attn);
@@ -529,9 +512,9 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
             return rc;
     }
 
-    // output RMSNorm + LM head + argmax
+    // output RMSNorm + LM head + argmax + next token
     if ((rc = launch_lm_head(S, S->h, logits, st))) return rc;
-    n += 2;
+    n += 1;
     if (nkernels) *nkernels = n;
     return ARC_OK;
 }
@@ -746,7 +729,7 @@ int arc_session_create(arc_model* m, uint32_t max_ctx, arc_session** out)
     S->s = static_cast<float*>(p);
     if ((rc = alloc(&p, size_t(d.vocab) * fl))) return rc;
     S->logits = static_cast<float*>(p);
-    const size_t heads_chunks = size_t(d.kv_heads) * S->max_chunks * (d.q_heads / d.kv_heads);
+    const size_t heads_chunks = size_t(d.kv_heads) * kMaxSplits * (d.q_heads / d.kv_heads);
     if ((rc = alloc(&p, heads_chunks * kHeadDim * fl))) return rc;
     S->apo = static_cast<float*>(p);
     if ((rc = alloc(&p, heads_chunks * 2 * fl))) return rc;
@@ -757,6 +740,9 @@ int arc_session_create(arc_model* m, uint32_t max_ctx, arc_session** out)
     S->best = static_cast<ArgBest*>(p);
     if ((rc = alloc(&p, sizeof(DecodeCtl)))) return rc;
     S->ctl = static_cast<DecodeCtl*>(p);
+    if ((rc = alloc(&p, kCounters * sizeof(uint32_t)))) return rc;
+    S->counters = static_cast<uint32_t*>(p);
+    if ((rc = check_hip(hipMemset(S->counters, 0, kCounters * sizeof(uint32_t)), "counters"))) return rc;
     if ((rc = alloc(&p, size_t(S->out_cap) * sizeof(uint32_t)))) return rc;
     S->out_tokens = static_cast<uint32_t*>(p);
     if ((rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&S->host_ctl), (size_t(max_ctx) + 1) * sizeof(DecodeCtl),

@@ -154,4 +154,53 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
+// ----------------------------------------------- cross-workgroup hand-off
+// Results one workgroup hands to another inside the same launch go through
+// memory with agent-scope relaxed atomics: stores write through the XCD's L2
+// (sc1) and loads bypass it, so no L2 writeback or invalidate is needed (an
+// agent-scope fence would write back the whole L2 of the XCD).  Nothing ever
+// waits for another workgroup: the last one to arrive does the follow-up.
+__device__ __forceinline__ void st_agent(float* p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p)
+{
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p)
+{
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Two consecutive floats (8-byte aligned) in one load.
+__device__ __forceinline__ float2 ld_agent2(const float* p)
+{
+    const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__builtin_bit_cast(float, uint32_t(v)), __builtin_bit_cast(float, uint32_t(v >> 32)));
+}
+
+// Called by every thread of the workgroup after its st_agent stores: waits
+// until they have reached memory, counts the workgroup in at `counter`, and
+// returns true in every thread of the one workgroup that arrives last out of
+// `n`.  That workgroup also resets the counter to zero for the next launch.
+// `flag` is a workgroup-shared word.
+__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t n, uint32_t* flag)
+{
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old + 1u == n;
+        if (last) st_agent(counter, 0u);
+        *flag = last ? 1u : 0u;
+    }
+    __syncthreads();
+    return *flag != 0u;
+}
+
 }  // namespace arc

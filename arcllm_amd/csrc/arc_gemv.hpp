@@ -57,7 +57,12 @@ enum Epi {
     EPI_VSTORE = 6
 };
 
-enum Flag : uint32_t { F_NORM = 1u, F_ACCUM = 2u, F_BIAS = 4u };
+// F_EMBED: x is row ctl->token of the Q4_K table `emb`, decoded while it is
+// staged (with F_NORM over the whole of x); workgroup 0 also writes the raw
+// row to h_out.  F_ARGNEXT (EPI_ARGMAX): the launch finishes the argmax
+// itself -- the last workgroup to arrive folds every workgroup's best and
+// advances the decode control block (token, position, step, out_tokens).
+enum Flag : uint32_t { F_NORM = 1u, F_ACCUM = 2u, F_BIAS = 4u, F_EMBED = 8u, F_ARGNEXT = 16u };
 
 struct GemvParams {
     const uint8_t* w0;
@@ -84,8 +89,13 @@ struct GemvParams {
     uint32_t kv_dim;          // QKROPE/VSTORE: cache row width (kv heads * 128)
     _Float16* cache;          // QKROPE/VSTORE: this layer's cache, [ctx][kv_dim]
     const float2* rope;       // QKROPE: (cos, sin) of pos * theta^(-2p/128), [ctx][64]
-    const DecodeCtl* ctl;     // QKROPE/VSTORE: current position
+    DecodeCtl* ctl;           // QKROPE/VSTORE: current position; F_EMBED: token; F_ARGNEXT: advanced
     float* y2;                // COLPART over all of K: y2 = res + fixed-order sum of the row's partials
+    const uint8_t* emb;       // F_EMBED: Q4_K token table, rows of nb super-blocks
+    float* h_out;             // F_EMBED: workgroup 0 writes the decoded row here
+    uint32_t* counter;        // F_ARGNEXT: arrival counter (zero between launches)
+    uint32_t* out_tokens;     // F_ARGNEXT: token of decode step ctl->step, if step < out_cap
+    uint32_t out_cap;
 };
 
 // ------------------------------------------------------------ block loads
@@ -515,6 +525,57 @@ __device__ void stage_x(float* lds, const float* __restrict__ x, uint32_t b0, ui
     }
 }
 
+// Elements e .. e+15 (16-aligned, so inside one 32-element sub-block) of a
+// Q4_K row, each decoded as the reference does: (d*sc)*q - dmin*mn with every
+// product and the difference rounded separately
+// (src/sa1_component_benchmark.cpp:105-116).
+__device__ __forceinline__ void emb_group(const uint8_t* __restrict__ row, uint32_t e, float4 (&q)[4])
+{
+#pragma clang fp contract(off)
+    const uint8_t* b = row + (e >> 8) * kQ4Bytes;
+    const uint32_t k0 = e & 255u, j = k0 >> 5;
+    const float d = f16_bits_to_f32(uint32_t(b[0]) | (uint32_t(b[1]) << 8));
+    const float dm = f16_bits_to_f32(uint32_t(b[2]) | (uint32_t(b[3]) << 8));
+    const uint8_t* sb = b + 4;
+    uint32_t sc, mn;
+    if (j < 4) {
+        sc = sb[j] & 63u;
+        mn = sb[j + 4] & 63u;
+    } else {
+        sc = (sb[j + 4] & 15u) | (uint32_t(sb[j - 4] >> 6) << 4);
+        mn = (sb[j + 4] >> 4) | (uint32_t(sb[j] >> 6) << 4);
+    }
+    const float t0 = d * float(sc);
+    const float t2 = dm * float(mn);
+    const uint32_t l64 = k0 & 63u;
+    const uint8_t* nib = b + 16 + (k0 >> 6) * 32 + (l64 & 31u);
+    const uint32_t sh = l64 < 32u ? 0u : 4u;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float t1 = t0 * float((uint32_t(nib[i]) >> sh) & 15u);
+        v[i] = t1 - t2;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+
+// One group of x: loaded from x, or (F_EMBED) decoded from the token's row.
+__device__ __forceinline__ void x_group(const float* __restrict__ x, const uint8_t* __restrict__ erow, uint32_t e,
+                                        float4 (&q)[4])
+{
+    if (erow)
+        emb_group(erow, e, q);
+    else
+        ld_group(x + e, q);
+}
+
+__device__ __forceinline__ void st_group(float* p, const float4 (&q)[4])
+{
+#pragma unroll
+    for (int i = 0; i < 4; ++i) reinterpret_cast<float4*>(p)[i] = q[i];
+}
+
 // RMSNorm fused into the staging of the whole of x (nbl super-blocks): the
 // thread's first group of x and of the norm weights is loaded once, its
 // squares enter the block-wide sum of squares (fp32, fixed order: the
@@ -522,20 +583,24 @@ __device__ void stage_x(float* lds, const float* __restrict__ x, uint32_t b0, ui
 // workgroup trees), and it is scaled and stored without a second read.
 template <int FMT, int NT>
 __device__ void stage_x_rms(float* lds, const float* __restrict__ x, uint32_t nbl, float eps,
-                            const float* __restrict__ normw, float* red)
+                            const float* __restrict__ normw, float* red, const uint8_t* __restrict__ erow,
+                            float* __restrict__ raw_out)
 {
     const uint32_t ng = nbl * 16u, gi0 = threadIdx.x;
     const bool have = gi0 < ng;
     float4 q0[4], w0[4];
     if (have) {
         const uint32_t e = group_elem<FMT>(0, gi0);
-        ld_group(x + e, q0);
+        x_group(x, erow, e, q0);
         ld_group(normw + e, w0);
+        if (raw_out) st_group(raw_out + e, q0);
     }
     float ss = 0.0f;
     for (uint32_t gi = gi0 + NT; gi < ng; gi += NT) {
+        const uint32_t e = group_elem<FMT>(0, gi);
         float4 q[4];
-        ld_group(x + group_elem<FMT>(0, gi), q);
+        x_group(x, erow, e, q);
+        if (raw_out) st_group(raw_out + e, q);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             ss = __builtin_fmaf(q[i].x, q[i].x, ss);
@@ -561,7 +626,7 @@ __device__ void stage_x_rms(float* lds, const float* __restrict__ x, uint32_t nb
     for (uint32_t gi = gi0 + NT; gi < ng; gi += NT) {
         const uint32_t e = group_elem<FMT>(0, gi);
         float4 q[4], w[4];
-        ld_group(x + e, q);
+        x_group(x, erow, e, q);
         ld_group(normw + e, w);
         scale_group(q, inv, w);
         put_group<FMT>(lds, gi, q);
@@ -574,8 +639,9 @@ __device__ __forceinline__ bool arg_better(float va, uint32_t ia, float vb, uint
 }
 
 // Argmax over a workgroup of (value, index) candidates, ties to the lowest
-// index, plus a sum of the non-finite counts.  Called by every thread.
-__device__ void wg_argmax(float bv, uint32_t bi, uint32_t nf, ArgBest* out)
+// index, plus a sum of the non-finite counts.  Called by every thread; every
+// thread receives the result.
+__device__ ArgBest wg_argmax(float bv, uint32_t bi, uint32_t nf)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -591,6 +657,7 @@ __device__ void wg_argmax(float bv, uint32_t bi, uint32_t nf, ArgBest* out)
     }
     __shared__ float sv[16];
     __shared__ uint32_t si[16], sn[16];
+    __shared__ ArgBest res;
     const int nw = blockDim.x >> 6;
     if (lane == 0) {
         sv[wave] = bv;
@@ -608,7 +675,52 @@ __device__ void wg_argmax(float bv, uint32_t bi, uint32_t nf, ArgBest* out)
             }
             c += sn[w];
         }
-        *out = ArgBest{b, i, c, 0u};
+        res = ArgBest{b, i, c, 0u};
+    }
+    __syncthreads();
+    return res;
+}
+
+__device__ __forceinline__ void st_agent_best(ArgBest* p, const ArgBest& b)
+{
+    uint32_t* w = reinterpret_cast<uint32_t*>(p);
+    st_agent(w, __builtin_bit_cast(uint32_t, b.val));
+    st_agent(w + 1, b.idx);
+    st_agent(w + 2, b.nonfinite);
+}
+
+// Second argmax stage inside the LM-head launch (F_ARGNEXT): the last
+// workgroup to arrive folds the n per-workgroup bests (read past the L2, as
+// the other workgroups wrote them) and advances the decode control block:
+// token = argmax (0 if every logit was non-finite), out_tokens[step] = token,
+// non-finite count, step + 1, position + 1.
+template <int NT>
+__device__ void argmax_finish(const GemvParams& p, uint32_t n)
+{
+    __shared__ uint32_t flag;
+    if (!arrive_last(p.counter, n, &flag)) return;
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu, nf = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += NT) {
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(p.best + i);
+        const float v = __builtin_bit_cast(float, ld_agent(w));
+        const uint32_t idx = ld_agent(w + 1);
+        nf += ld_agent(w + 2);
+        if (idx != 0xffffffffu && arg_better(v, idx, bv, bi)) {
+            bv = v;
+            bi = idx;
+        }
+    }
+    const ArgBest r = wg_argmax(bv, bi, nf);
+    if (threadIdx.x == 0) {
+        DecodeCtl* ctl = p.ctl;
+        const uint32_t tok = r.idx == 0xffffffffu ? 0u : r.idx;
+        const uint32_t step = ctl->step;
+        if (step < p.out_cap) p.out_tokens[step] = tok;
+        ctl->token = tok;
+        ctl->nonfinite += r.nonfinite;
+        ctl->step = step + 1;
+        ctl->pos += 1;
     }
 }
 
@@ -640,7 +752,9 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
     static_assert(W == 4 || W == 8, "4 or 8 waves per workgroup");
     constexpr int NT = W * kWave;
     constexpr int PF = ring_depth<FMT, EPI>();  // register buffers in the prefetch ring
-    extern __shared__ float lds[];
+    // 16-byte aligned: the staged x is read as float4; the base follows the
+    // kernel's static LDS, whose size is not a multiple of 16 in general
+    extern __shared__ __align__(16) float lds[];
     __shared__ float red[W];
     constexpr int NMAT = (EPI == EPI_SWIGLU) ? 2 : 1;
     constexpr int N = NMAT * RPL;
@@ -750,7 +864,16 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
     load_ep(0);
 
     if ((p.flags & F_NORM) && kb == 0 && nbl == p.nb) {
-        stage_x_rms<FMT, NT>(lds, p.x, nbl, p.eps, p.normw, red);
+        const uint8_t* erow = nullptr;
+        float* raw = nullptr;
+        // the embedding path exists only in the q/k/v epilogues (the first
+        // layer's projections): its code costs the other GEMVs registers
+        if constexpr (EPI == EPI_QKROPE || EPI == EPI_VSTORE)
+            if (p.flags & F_EMBED) {
+                erow = p.emb + uint64_t(p.ctl->token) * p.nb * kQ4Bytes;
+                if (bx == 0) raw = p.h_out;
+            }
+        stage_x_rms<FMT, NT>(lds, p.x, nbl, p.eps, p.normw, red, erow, raw);
     } else {
         float inv = 1.0f;
         if (p.flags & F_NORM) inv = rms_inv<NT>(p.x, p.nb * kQK, p.eps, red);
@@ -899,7 +1022,15 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
     for (int k = 0; k < PF - 1; ++k)
         if (s + k < S) step(buf[(k + PF - 1) % PF], buf[k]);
 
-    if constexpr (EPI == EPI_ARGMAX) wg_argmax(best_v, best_i, nonfinite, p.best + bx);
+    if constexpr (EPI == EPI_ARGMAX) {
+        const ArgBest r = wg_argmax(best_v, best_i, nonfinite);
+        if (p.flags & F_ARGNEXT) {
+            if (threadIdx.x == 0) st_agent_best(p.best + bx, r);
+            argmax_finish<NT>(p, gx);
+        } else if (threadIdx.x == 0) {
+            p.best[bx] = r;
+        }
+    }
 }
 
 template <int FMT, int BS, int RPL, int EPI, int W>
@@ -915,7 +1046,7 @@ struct Cfg {
 
 inline int tile_rows(const Cfg& c) { return (kWave / (4 * c.bs)) * c.rpl; }
 
-static int cu_count()
+inline int cu_count()
 {
     static int n = 0;
     static std::once_flag once;
@@ -949,8 +1080,11 @@ int occupancy(size_t lds, uint32_t panel)
     return occ[slot];
 }
 
-static thread_local int g_wg_per_cu = 0;  // tuning override of resident workgroups per CU
-static thread_local bool g_dry_run = false;  // size grids and fill caches without launching
+// Launch state shared by every translation unit that includes this header
+// (inline variables: one definition in the library, so a launch helper
+// instantiated in one source file sees the flag another one set).
+inline thread_local int g_wg_per_cu = 0;     // tuning override of resident workgroups per CU
+inline thread_local bool g_dry_run = false;  // size grids and fill caches without launching
 
 template <int FMT, int EPI, int BS, int RPL, int W = kWaves>
 hipError_t launch_one(GemvParams p, uint32_t splits, hipStream_t s, uint32_t* grid_x)
@@ -973,8 +1107,8 @@ hipError_t launch_one(GemvParams p, uint32_t splits, hipStream_t s, uint32_t* gr
 }
 
 // Forced configuration for tuning sweeps (bs = 0: automatic; waves = 0: automatic).
-static thread_local Cfg g_force{0, 0, 0};
-static thread_local int g_force_waves = 0;
+inline thread_local Cfg g_force{0, 0, 0};
+inline thread_local int g_force_waves = 0;
 
 // Q6_K layouts with 4 rows per lane (256 VGPRs plus spills into AGPRs) are
 // not built: the 2-quad one took a GPU memory fault once, with no cause found

@@ -108,9 +108,7 @@ __global__ __launch_bounds__(1024) void k_argmax_final(const ArgBest* __restrict
             nf += b[k].nonfinite;
         }
     }
-    __shared__ ArgBest res;
-    wg_argmax(bv, bi, nf, &res);
-    __syncthreads();
+    const ArgBest res = wg_argmax(bv, bi, nf);
     if (threadIdx.x == 0) {
         out[0] = (res.idx == 0xffffffffu) ? 0u : res.idx;
         out[1] = res.nonfinite;

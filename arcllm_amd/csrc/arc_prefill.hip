@@ -406,7 +406,7 @@ template <int FMT, int MB, int NF, bool SWIGLU>
 __device__ __forceinline__ void pf_gemm_body(const PfGemm& p, uint32_t tile)
 {
     static_assert(!SWIGLU || NF == 2, "SwiGLU pairs a gate and an up row per lane");
-    extern __shared__ _Float16 ash[];  // [2][MB*32][kPfLd]
+    extern __shared__ __align__(16) _Float16 ash[];  // [2][MB*32][kPfLd]
     constexpr int kStage = MB * 32 * kPfLd;
     constexpr int kBB = FMT == kFmtQ4 ? kQ4Bytes : kQ6Bytes;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1099,7 +1099,7 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
         }
         if (pass + 1 == passes) {
             if ((rc = launch_lm_head(S, pf->h + uint64_t(M - 1) * H, logits, st))) return rc;
-            nk += 2;
+            nk += 1;
         }
     }
     pf->kernels = nk;

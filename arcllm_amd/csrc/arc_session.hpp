@@ -12,9 +12,16 @@
 namespace arc {
 
 constexpr int kHeadDim = 128;
-constexpr int kChunk = 64;       // positions per attention workgroup
+constexpr int kChunk = 64;       // positions per attention chunk
 constexpr int kMaxHpk = 8;       // q heads per kv head
 constexpr int kMaxChunks = 512;  // contexts up to 32768 positions
+constexpr int kMaxSplits = 64;   // attention workgroups per kv head
+// Arrival counters of the decode step's last-arriver hand-offs (session
+// memory, zero between launches): one per kv head for attention, one for
+// the LM-head argmax.
+constexpr int kCounterAttn = 0;
+constexpr int kCounterLmHead = 64;
+constexpr int kCounters = 65;
 
 struct PrefillBufs;                  // arc_prefill.hip
 void destroy_prefill(PrefillBufs*);  // arc_prefill.hip
@@ -51,7 +58,8 @@ struct arc_session {
     _Float16* kcache = nullptr;  // [layers][max_ctx][kv_dim]
     _Float16* vcache = nullptr;
     float *h = nullptr, *h1 = nullptr, *q = nullptr, *attn = nullptr, *s = nullptr, *logits = nullptr;
-    float *apo = nullptr, *apml = nullptr;
+    float *apo = nullptr, *apml = nullptr;  // attention split partials [kv_heads][kMaxSplits][hpk][...]
+    uint32_t* counters = nullptr;            // kCounters arrival counters
     float2* rope = nullptr;  // [max_ctx][64] (cos, sin) of pos * theta^(-2p/128)
     arc::ArgBest* best = nullptr;
     uint32_t best_cap = 0;

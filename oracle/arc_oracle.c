@@ -697,3 +697,114 @@ int orc_decode_step_ex(const orc_model *m, uint16_t *kc, uint16_t *vc, uint32_t 
     free(h); free(xn); free(q); free(kk); free(vv); free(at); free(o); free(g); free(u); free(sw);
     return 0;
 }
+
+
+/* ---- the prompt pass batched over n positions ---- */
+
+/* Y[i][r] = sum_k w[r][k] * X[i][k] for i < n, each sum in the order of
+ * orc_gemv_r64_xd (f16 = 0) or orc_gemv_r64_f16 (f16 != 0): every weight row
+ * is decoded once and applied to all n rows, the n sums of a row advance
+ * together over k (independent accumulators, so the order within each sum is
+ * unchanged and the results are bit-identical to n single GEMVs). */
+static int gemm_rows(int qtype, const uint8_t *w, uint32_t rows, uint32_t K, uint32_t n,
+                     const double *X, int f16, double *Y)
+{
+    size_t rb, bb;
+    if (row_bytes(qtype, K, &rb, &bb)) return -1;
+    double *XT = malloc(sizeof(double) * (size_t)K * n);
+    if (!XT) return -2;
+    for (uint32_t i = 0; i < n; ++i)
+        for (uint32_t k = 0; k < K; ++k) {
+            const double x = X[(size_t)i * K + k];
+            XT[(size_t)k * n + i] = f16 ? (double)orc_half_to_float(orc_float_to_half_rne((float)x)) : x;
+        }
+    int fail = 0;
+    long r;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 16)
+#endif
+    for (r = 0; r < (long)rows; ++r) {
+        double *acc = malloc(sizeof(double) * n);
+        if (!acc) { fail = 1; continue; }
+        for (uint32_t i = 0; i < n; ++i) acc[i] = 0.0;
+        const uint8_t *row = w + (size_t)r * rb;
+        float wb[ORC_QK];
+        for (uint32_t k0 = 0; k0 < K; k0 += ORC_QK) {
+            decode_block(qtype, row + (k0 / ORC_QK) * bb, wb);
+            for (uint32_t k = 0; k < ORC_QK; ++k) {
+                const double wk = f16 ? (double)orc_half_to_float(orc_float_to_half_rne(wb[k])) : (double)wb[k];
+                const double *xt = XT + (size_t)(k0 + k) * n;
+                for (uint32_t i = 0; i < n; ++i) acc[i] += wk * xt[i];
+            }
+        }
+        for (uint32_t i = 0; i < n; ++i) Y[(size_t)i * rows + r] = acc[i];
+        free(acc);
+    }
+    free(XT);
+    return fail ? -2 : 0;
+}
+
+/* n calls of orc_decode_step_ex with teacher forcing (tokens[i] at position
+ * pos0 + i), restated layer by layer over all n positions at once: position
+ * i's attention reads cache rows 0 .. pos0 + i of the layer, all written
+ * before it, so every value equals the stepwise oracle's bit for bit.
+ * src/arcllm_v1_runtime.cpp:340-369 (build_prefill, last-token LM head).
+ * Returns the logits of the last position. */
+int orc_prompt_pass(const orc_model *m, uint16_t *kc, uint16_t *vc, uint32_t max_ctx, uint32_t pos0, uint32_t n,
+                    const uint32_t *tokens, int f16_operands, double *logits)
+{
+    const uint32_t H = m->hidden, KVD = m->kv_heads * m->head_dim, F = m->ffn;
+    if (n == 0u || (uint64_t)pos0 + n > max_ctx || m->layers > ORC_MAX_LAYERS) return -1;
+    for (uint32_t i = 0; i < n; ++i)
+        if (tokens[i] >= m->vocab) return -1;
+    const size_t nH = (size_t)n * H, nK = (size_t)n * KVD, nF = (size_t)n * F;
+    double *h = malloc(sizeof(double) * nH), *xn = malloc(sizeof(double) * nH), *q = malloc(sizeof(double) * nH);
+    double *kk = malloc(sizeof(double) * nK), *vv = malloc(sizeof(double) * nK), *at = malloc(sizeof(double) * nH);
+    double *o = malloc(sizeof(double) * nH), *g = malloc(sizeof(double) * nF), *u = malloc(sizeof(double) * nF);
+    double *sw = malloc(sizeof(double) * nF);
+    int rc = 0;
+    if (!h || !xn || !q || !kk || !vv || !at || !o || !g || !u || !sw) { rc = -2; goto done; }
+    const size_t erow = (size_t)(H / ORC_QK) * ORC_Q4K_BLOCK_BYTES;
+    for (uint32_t i = 0; i < n; ++i)
+        for (uint32_t e = 0; e < H; ++e)
+            h[(size_t)i * H + e] = (double)orc_q4k_weight(m->emb + (size_t)tokens[i] * erow + (e / ORC_QK) * ORC_Q4K_BLOCK_BYTES,
+                                                          e % ORC_QK);
+    for (uint32_t l = 0; l < m->layers; ++l) {
+        uint16_t *kl = kc + (size_t)l * max_ctx * KVD, *vl = vc + (size_t)l * max_ctx * KVD;
+        for (uint32_t i = 0; i < n; ++i) orc_rmsnorm_f64(h + (size_t)i * H, m->attn_norm[l], H, m->eps, xn + (size_t)i * H);
+        if ((rc = gemm_rows(ORC_Q4_K, m->q[l], H, H, n, xn, f16_operands, q))) goto done;
+        if ((rc = gemm_rows(ORC_Q4_K, m->k[l], KVD, H, n, xn, f16_operands, kk))) goto done;
+        if ((rc = gemm_rows(m->v_type[l], m->v[l], KVD, H, n, xn, f16_operands, vv))) goto done;
+        for (uint32_t i = 0; i < n; ++i) {
+            double *qi = q + (size_t)i * H, *ki = kk + (size_t)i * KVD, *vi = vv + (size_t)i * KVD;
+            const uint32_t pos = pos0 + i;
+            for (uint32_t e = 0; e < H; ++e) qi[e] += (double)m->qb[l][e];
+            for (uint32_t e = 0; e < KVD; ++e) {
+                ki[e] += (double)m->kb[l][e];
+                vi[e] += (double)m->vb[l][e];
+            }
+            orc_rope_f64(qi, m->q_heads, m->head_dim, pos, m->theta);
+            orc_rope_f64(ki, m->kv_heads, m->head_dim, pos, m->theta);
+            for (uint32_t e = 0; e < KVD; ++e) {
+                kl[(size_t)pos * KVD + e] = orc_float_to_half_rne((float)ki[e]);
+                vl[(size_t)pos * KVD + e] = orc_float_to_half_rne((float)vi[e]);
+            }
+        }
+        for (uint32_t i = 0; i < n; ++i)
+            orc_attention_decode_f64(q + (size_t)i * H, kl, vl, pos0 + i, m->q_heads, m->kv_heads, m->head_dim,
+                                     at + (size_t)i * H);
+        if ((rc = gemm_rows(ORC_Q4_K, m->o[l], H, H, n, at, f16_operands, o))) goto done;
+        for (size_t e = 0; e < nH; ++e) h[e] += o[e];
+        for (uint32_t i = 0; i < n; ++i) orc_rmsnorm_f64(h + (size_t)i * H, m->ffn_norm[l], H, m->eps, xn + (size_t)i * H);
+        if ((rc = gemm_rows(ORC_Q4_K, m->gate[l], F, H, n, xn, f16_operands, g))) goto done;
+        if ((rc = gemm_rows(ORC_Q4_K, m->up[l], F, H, n, xn, f16_operands, u))) goto done;
+        for (uint32_t i = 0; i < n; ++i) orc_swiglu_f64(g + (size_t)i * F, u + (size_t)i * F, F, sw + (size_t)i * F);
+        if ((rc = gemm_rows(m->down_type[l], m->down[l], H, F, n, sw, f16_operands, o))) goto done;
+        for (size_t e = 0; e < nH; ++e) h[e] += o[e];
+    }
+    orc_rmsnorm_f64(h + (size_t)(n - 1) * H, m->out_norm, H, m->eps, xn);
+    rc = orc_gemv_r64_xd(ORC_Q6_K, m->out, m->vocab, H, xn, logits);
+done:
+    free(h); free(xn); free(q); free(kk); free(vv); free(at); free(o); free(g); free(u); free(sw);
+    return rc;
+}

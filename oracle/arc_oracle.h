@@ -112,6 +112,12 @@ int orc_decode_step(const orc_model *m, uint16_t *kc, uint16_t *vc, uint32_t max
  * batched MFMA prompt pass. */
 int orc_decode_step_ex(const orc_model *m, uint16_t *kc, uint16_t *vc, uint32_t max_ctx, uint32_t pos,
                        uint32_t token, int f16_operands, double *logits);
+/* The same as n calls of orc_decode_step_ex with tokens[i] at position
+ * pos0 + i (teacher forcing), computed layer by layer over all n positions
+ * (each weight row decoded once per layer); bit-identical results.  Returns
+ * the logits of the last position. */
+int orc_prompt_pass(const orc_model *m, uint16_t *kc, uint16_t *vc, uint32_t max_ctx, uint32_t pos0, uint32_t n,
+                    const uint32_t *tokens, int f16_operands, double *logits);
 
 #ifdef __cplusplus
 }

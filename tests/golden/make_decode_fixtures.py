@@ -13,9 +13,10 @@ decode7b_greedy.npz -- the Qwen2.5-7B-shaped random-init model (seed
     t4096_logits              the first step's full logits at T = 4096 (fp32)
 
 prefill7b_256.npz -- the same model shape (seed PREFILL_SEED), the 256-token
-  prompt (7919 i + 13) mod vocab at positions 0..255, run through the oracle
-  once with fp16 GEMM operands (the rounding of the MFMA prompt pass) and once
-  exactly in fp64:
+  prompt (7919 i + 13) mod vocab at positions 0..255, run through the oracle's
+  prompt pass (orc_prompt_pass: bit-identical to stepping the tokens one by
+  one) once with fp16 GEMM operands (the rounding of the MFMA prompt pass) and
+  once exactly in fp64:
     f16_logits                last position's logits, fp16-operand oracle (fp32)
     f16_next, f16_second, f16_margin, f16_scale
     exact_next, exact_second, exact_margin, exact_scale, exact_top_idx/val
@@ -102,11 +103,11 @@ def make_prefill(path: str) -> None:
     prompt = prompt_ids(d.vocab)
     o16 = orc.DecodeOracle(d, T, PF_MAX_CTX, f16_operands=True)
     o64 = orc.DecodeOracle(d, T, PF_MAX_CTX)
-    for i, t in enumerate(prompt):
-        l16 = o16.step(int(t), i)
-        l64 = o64.step(int(t), i)
-        if i % 16 == 15:
-            _log(f"prefill oracle position {i}")
+    # layer by layer over all positions: bit-identical to stepping each token
+    l16 = o16.prompt(prompt, 0)
+    _log("prefill: fp16-operand oracle done")
+    l64 = o64.prompt(prompt, 0)
+    _log("prefill: exact oracle done")
     out = {"seed": np.uint64(PREFILL_SEED), "prompt": prompt, "max_ctx": np.uint32(PF_MAX_CTX)}
     for name, lg in (("f16", l16), ("exact", l64)):
         order = np.argsort(-lg, kind="stable")

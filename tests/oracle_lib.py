@@ -79,6 +79,7 @@ def oracle() -> C.CDLL:
             "orc_attention_decode_f64": ([_P, _P, _P, _U32, _U32, _U32, _U32, _P], None),
             "orc_decode_step": ([C.POINTER(OrcModel), _P, _P, _U32, _U32, _U32, _P], C.c_int),
             "orc_decode_step_ex": ([C.POINTER(OrcModel), _P, _P, _U32, _U32, _U32, C.c_int, _P], C.c_int),
+            "orc_prompt_pass": ([C.POINTER(OrcModel), _P, _P, _U32, _U32, _U32, _P, C.c_int, _P], C.c_int),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -254,6 +255,16 @@ class DecodeOracle:
         logits = np.empty(self.dims.vocab, np.float64)
         rc = oracle().orc_decode_step_ex(C.byref(self.m), _p(self.kc), _p(self.vc), self.max_ctx, pos, token,
                                          self.f16, _p(logits))
+        assert rc == 0
+        return logits
+
+    def prompt(self, tokens, pos0=0):
+        """tokens[i] at position pos0 + i (teacher forcing), all positions
+        layer by layer (bit-identical to stepping); logits of the last one."""
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
+        logits = np.empty(self.dims.vocab, np.float64)
+        rc = oracle().orc_prompt_pass(C.byref(self.m), _p(self.kc), _p(self.vc), self.max_ctx, pos0, len(toks),
+                                      _p(toks), self.f16, _p(logits))
         assert rc == 0
         return logits
 

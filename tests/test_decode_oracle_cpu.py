@@ -134,3 +134,29 @@ def test_element_products_are_exact_in_fp32(qtype):
                 q = O.orc_q6k_code(p, k, orc.C.byref(s))
                 prod = d * s.value * q
             assert np.float64(np.float32(prod)) == prod
+
+
+@pytest.mark.parametrize("f16", [0, 1])
+def test_prompt_pass_oracle_equals_stepwise_oracle(f16):
+    """orc_prompt_pass (layer by layer over all positions) against
+    orc_decode_step_ex called per position with teacher forcing: last logits
+    and every cache row bit-identical; a planted change in one prompt token
+    changes the logits."""
+    d = tiny_dims(layers=3)
+    T = arc.synth_model_tensors(d, 0x5EED)
+    max_ctx, pos0 = 64, 5
+    prompt = (np.arange(23, dtype=np.uint32) * 131 + 7) % d.vocab
+    a = orc.DecodeOracle(d, T, max_ctx, f16_operands=bool(f16))
+    a.fill_kv(pos0, 3, arc.synth_normal)
+    b = orc.DecodeOracle(d, T, max_ctx, f16_operands=bool(f16))
+    b.fill_kv(pos0, 3, arc.synth_normal)
+    la = a.prompt(prompt, pos0)
+    for i, t in enumerate(prompt):
+        lb = b.step(int(t), pos0 + i)
+    assert np.array_equal(la.view(np.uint64), lb.view(np.uint64))
+    assert np.array_equal(a.kc, b.kc) and np.array_equal(a.vc, b.vc)
+    c = orc.DecodeOracle(d, T, max_ctx, f16_operands=bool(f16))
+    c.fill_kv(pos0, 3, arc.synth_normal)
+    planted = prompt.copy()
+    planted[10] = (planted[10] + 1) % d.vocab
+    assert not np.array_equal(c.prompt(planted, pos0), la)

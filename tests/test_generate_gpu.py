@@ -84,9 +84,9 @@ def test_generate_cli_matches_oracle(tmp_path):
     assert len(gpu) == max_new
     assert tokens_match(gpu, ref, second, margins, scale) >= max_new // 2
     st = res["stats"]
-    per_step = 3 + 6 * d.layers
+    per_step = 1 + 5 * d.layers
     # batched prompt pass: embed + first norm, 8 launches per layer, LM head + next token
-    assert st["prefill_dispatches"] == 8 * d.layers + 4 and st["prefill_submits"] == 1
+    assert st["prefill_dispatches"] == 8 * d.layers + 3 and st["prefill_submits"] == 1
     assert st["decode_dispatches_per_step"] == per_step and st["decode_submits_per_step"] == 1
     # layer 1's ffn_down is Q4_K: within the evidence scope and with
     # max_new - 1 future tokens (>= the P1 threshold) the policy acquires the EXEC148 image by P1

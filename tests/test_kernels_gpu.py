@@ -292,8 +292,10 @@ def _lmhead(qtype, w, rows, K, h, nw, eps=1e-6, logits=True):
     return int(o[0]), int(o[1]), (lg.download(np.float32) if logits else None)
 
 
-@pytest.mark.parametrize("rows", [4097, 30000])
+@pytest.mark.parametrize("rows", [4097, 30000, 152064])
 def test_lmhead_argmax(rows):
+    """Config 2 (at 152,064 rows the Qwen2.5-7B vocabulary): RMSNorm + Q6_K LM
+    head + argmax, every logit against the fp64 oracle, the token exactly."""
     K = 3584
     w = packed(arc.Q6_K, rows, K, 60)
     h = arc.synth_normal(SEED, 61, K)

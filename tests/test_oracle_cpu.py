@@ -369,6 +369,29 @@ def test_r0_bias_and_splitk_consistency():
     assert np.array_equal(mt.view(np.uint32), r0.view(np.uint32))
 
 
+@pytest.mark.parametrize("qtype", [orc.Q4_K, orc.Q6_K])
+def test_splitk_partials_are_r64_of_their_column_slices(qtype):
+    """Brute force: partial j of orc_gemv_splitk_r64 is, bit for bit, R64 of
+    the sub-tensor made of the super-block columns [j*bps, min((j+1)*bps, nb))
+    of every row against the matching slice of x; splits past the last
+    column are zero."""
+    rows, K = 9, 2560
+    nb, bb = K // 256, orc.BLOCK_BYTES[qtype]
+    w, x = _synthetic(qtype, rows, K, 17)
+    w2 = w.reshape(rows, nb * bb)
+    for splits in (1, 3, 4, 7, 10):
+        bps = -(-nb // splits)
+        part = orc.splitk_r64(qtype, w, rows, K, splits, x)
+        for j in range(splits):
+            b0, b1 = j * bps, min((j + 1) * bps, nb)
+            if b0 >= nb:
+                assert not part[j].any()
+                continue
+            sub = np.ascontiguousarray(w2[:, b0 * bb:b1 * bb]).ravel()
+            ref = orc.gemv_r64(qtype, sub, rows, (b1 - b0) * 256, np.ascontiguousarray(x[b0 * 256:b1 * 256]))
+            assert np.array_equal(part[j].view(np.uint64), ref.view(np.uint64)), (splits, j)
+
+
 # ----------------------------------------------------- norm / act / rope
 def test_rmsnorm_matches_formula():
     rng = np.random.default_rng(8)

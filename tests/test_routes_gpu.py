@@ -71,7 +71,7 @@ def test_session_route_down_switches_and_matches_oracle():
         s.fill_kv(ctx, kv_seed)
         toks, nf = s.decode(77, ctx, steps)
         assert nf == 0
-        assert s.kernels_per_step == 3 + 6 * d.layers
+        assert s.kernels_per_step == 1 + 5 * d.layers
         results[name] = toks
         _log(f"route {name}: {toks.tolist()}")
         assert _match(toks, ref, second, margins, scale) >= steps // 2, name
