@@ -88,9 +88,9 @@ def test_policy_trace_identical_to_reference_build(trace_exe, tmp_path):
 def test_policy_trace_catches_a_planted_threshold_mistake(trace_exe, tmp_path):
     with open(os.path.join(HOST, "policy_v4.cpp")) as f:
         src = f.read()
-    needle = "r.future_reuse_units < th->minimum_reuse_units"
+    needle = "s.req.future_reuse_units < bar->minimum_reuse_units"
     assert src.count(needle) == 1
-    src = src.replace(needle, "r.future_reuse_units <= th->minimum_reuse_units")
+    src = src.replace(needle, "s.req.future_reuse_units <= bar->minimum_reuse_units")
     src = src.replace('"../../include/', f'"{ROOT}/include/')
     planted = tmp_path / "policy_planted.cpp"
     planted.write_text(src)
