@@ -60,6 +60,7 @@ _SIGS = {
     "arc_device_info": [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t],
     "arc_malloc": [C.POINTER(_P), C.c_size_t],
     "arc_free": [_P],
+    "arc_device_allocations": [C.POINTER(_U64)],
     "arc_memcpy_htod": [_P, _P, C.c_size_t, _P],
     "arc_memcpy_dtoh": [_P, _P, C.c_size_t, _P],
     "arc_memcpy_dtod": [_P, _P, C.c_size_t, _P],
@@ -108,6 +109,11 @@ class ModelDims(C.Structure):
                 ("v_type", C.c_int32 * MAX_LAYERS), ("down_type", C.c_int32 * MAX_LAYERS)]
 
 
+class Residency(C.Structure):
+    _fields_ = [("weight_bytes", _U64), ("model_arena_bytes", _U64), ("exec148_reserve_bytes", _U64),
+                ("kv_bytes", _U64), ("working_bytes", _U64), ("total_bytes", _U64)]
+
+
 _SIGS.update({
     "arc_model_dims_qwen25_7b": [C.POINTER(ModelDims)],
     "arc_model_tensor_info": [C.POINTER(ModelDims), C.c_int, C.c_int, C.POINTER(C.c_int), C.POINTER(_U32),
@@ -117,7 +123,9 @@ _SIGS.update({
     "arc_model_create_synthetic": [C.POINTER(ModelDims), _U64, C.POINTER(_P)],
     "arc_model_destroy": [_P],
     "arc_model_weight_bytes": [_P],
+    "arc_model_exec148_reserve": [_P, C.POINTER(_P), C.POINTER(_U64), C.POINTER(_U32)],
     "arc_session_create": [_P, _U32, C.POINTER(_P)],
+    "arc_session_residency": [_P, C.POINTER(Residency)],
     "arc_session_destroy": [_P],
     "arc_session_kv": [_P, _U32, C.POINTER(_P), C.POINTER(_P)],
     "arc_session_fill_kv": [_P, _U32, _U64],
@@ -468,6 +476,12 @@ class Model:
         check(lib().arc_model_tensor_device(self.handle, layer, which, C.byref(ptr)))
         return int(ptr.value)
 
+    def exec148_reserve(self) -> tuple[int, int, int]:
+        """(device base, slot stride, slots) of the model's EXEC148 reserve."""
+        base, stride, slots = _P(), _U64(0), _U32(0)
+        check(lib().arc_model_exec148_reserve(self.handle, C.byref(base), C.byref(stride), C.byref(slots)))
+        return int(base.value or 0), int(stride.value), int(slots.value)
+
     def close(self) -> None:
         if getattr(self, "handle", None):
             if _lib is not None:
@@ -479,6 +493,13 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+def device_allocations() -> int:
+    """Device allocations the library has made in this process."""
+    n = _U64(0)
+    check(lib().arc_device_allocations(C.byref(n)))
+    return int(n.value)
 
 
 class Session:
@@ -533,6 +554,12 @@ class Session:
     @property
     def kernels_per_step(self) -> int:
         return int(lib().arc_session_kernels_per_step(self.handle))
+
+    def residency(self) -> dict:
+        """The planned bytes of the session and its model (arc_session_residency)."""
+        r = Residency()
+        check(lib().arc_session_residency(self.handle, C.byref(r)))
+        return {name: int(getattr(r, name)) for name, _ in Residency._fields_}
 
     def close(self) -> None:
         if getattr(self, "handle", None):

@@ -606,48 +606,63 @@ int arc_model_create(const arc_model_dims* dims, const void* const* tensors, arc
     std::unique_ptr<arc_model> M(new (std::nothrow) arc_model);
     if (!M) return set_error(ARC_ERR_OUT_OF_MEMORY, "host allocation");
     M->dims = *dims;
-    auto upload = [&](int layer, int which, const void** dst) -> int {
+    M->layers.resize(dims->layers);
+
+    // The arena: every tensor in slot order (globals, then layer by layer),
+    // 256 bytes of slack after the last (kernels read 16-byte vectors past a
+    // row's end), then the EXEC148 reserve.
+    struct Upload {
+        const void* src;
+        uint64_t bytes;
+        const void* dev = nullptr;
+    };
+    const size_t nt = size_t(ARC_T_GLOBAL_COUNT) + size_t(dims->layers) * ARC_T_LAYER_COUNT;
+    std::vector<Upload> up(nt);
+    ArenaPlan plan;
+    for (size_t i = 0; i < nt; ++i) {
+        const int layer = i < size_t(ARC_T_GLOBAL_COUNT) ? -1 : int((i - ARC_T_GLOBAL_COUNT) / ARC_T_LAYER_COUNT);
+        const int which = i < size_t(ARC_T_GLOBAL_COUNT) ? int(i) : int((i - ARC_T_GLOBAL_COUNT) % ARC_T_LAYER_COUNT);
         int qtype;
         uint32_t rows, K;
-        uint64_t bytes;
-        int r = arc_model_tensor_info(dims, layer, which, &qtype, &rows, &K, &bytes);
-        if (r) return r;
-        const size_t idx = layer < 0 ? size_t(which) : size_t(ARC_T_GLOBAL_COUNT) + size_t(layer) * ARC_T_LAYER_COUNT + which;
-        const void* src = tensors[idx];
-        if (!src) return set_error(ARC_ERR_INVALID_ARGUMENT, "tensor %zu is null", idx);
-        void* p = nullptr;
-        if ((r = check_hip(hipMalloc(&p, bytes + 256), "hipMalloc weights"))) return r;  // slack: 16 B loads
-        M->allocations.push_back(p);
-        if ((r = check_hip(hipMemcpy(p, src, bytes, hipMemcpyHostToDevice), "upload weights"))) return r;
-        M->weight_bytes += bytes;
-        *dst = p;
-        return ARC_OK;
-    };
-    const void* tmp = nullptr;
-    if ((rc = upload(-1, ARC_T_TOKEN_EMBD, &tmp))) return rc;
-    M->emb = static_cast<const uint8_t*>(tmp);
-    if ((rc = upload(-1, ARC_T_OUTPUT, &tmp))) return rc;
-    M->out = static_cast<const uint8_t*>(tmp);
-    if ((rc = upload(-1, ARC_T_OUTPUT_NORM, &tmp))) return rc;
-    M->out_norm = static_cast<const float*>(tmp);
-    M->layers.resize(dims->layers);
+        if ((rc = arc_model_tensor_info(dims, layer, which, &qtype, &rows, &K, &up[i].bytes))) return rc;
+        if (!(up[i].src = tensors[i])) return set_error(ARC_ERR_INVALID_ARGUMENT, "tensor %zu is null", i);
+        plan.place(&up[i].dev, up[i].bytes);
+        M->weight_bytes += up[i].bytes;
+    }
+    plan.pad(256);
+    for (uint32_t l = 0; l < dims->layers; ++l)
+        if (dims->down_type[l] == ARC_Q4_K) ++M->e148_slots;
+    if (M->e148_slots) {
+        M->e148_stride = ArenaPlan::round_up(exec148_image_bytes(dims->hidden, dims->ffn));
+        plan.place(&M->e148_base, M->e148_stride * M->e148_slots);
+    }
+    plan.pad(4096);  // nothing near the allocation's end is read past it
+    M->arena_bytes = plan.bytes();
+    if ((rc = plan.commit(&M->arena, "model arena"))) return rc;
+    for (const Upload& u : up)
+        if ((rc = check_hip(hipMemcpy(const_cast<void*>(u.dev), u.src, u.bytes, hipMemcpyHostToDevice),
+                            "upload weights")))
+            return rc;
+
+    auto at = [&](int layer, int which) { return up[size_t(ARC_T_GLOBAL_COUNT) + size_t(layer) * ARC_T_LAYER_COUNT + which].dev; };
+    M->emb = static_cast<const uint8_t*>(up[ARC_T_TOKEN_EMBD].dev);
+    M->out = static_cast<const uint8_t*>(up[ARC_T_OUTPUT].dev);
+    M->out_norm = static_cast<const float*>(up[ARC_T_OUTPUT_NORM].dev);
     for (uint32_t l = 0; l < dims->layers; ++l) {
         Layer& L = M->layers[l];
-        const void* t[ARC_T_LAYER_COUNT] = {};
-        for (int w = 0; w < ARC_T_LAYER_COUNT; ++w)
-            if ((rc = upload(int(l), w, &t[w]))) return rc;
-        L.attn_norm = static_cast<const float*>(t[ARC_T_ATTN_NORM]);
-        L.q = static_cast<const uint8_t*>(t[ARC_T_ATTN_Q]);
-        L.k = static_cast<const uint8_t*>(t[ARC_T_ATTN_K]);
-        L.v = static_cast<const uint8_t*>(t[ARC_T_ATTN_V]);
-        L.qb = static_cast<const float*>(t[ARC_T_ATTN_Q_BIAS]);
-        L.kb = static_cast<const float*>(t[ARC_T_ATTN_K_BIAS]);
-        L.vb = static_cast<const float*>(t[ARC_T_ATTN_V_BIAS]);
-        L.o = static_cast<const uint8_t*>(t[ARC_T_ATTN_O]);
-        L.ffn_norm = static_cast<const float*>(t[ARC_T_FFN_NORM]);
-        L.gate = static_cast<const uint8_t*>(t[ARC_T_FFN_GATE]);
-        L.up = static_cast<const uint8_t*>(t[ARC_T_FFN_UP]);
-        L.down = static_cast<const uint8_t*>(t[ARC_T_FFN_DOWN]);
+        const int li = int(l);
+        L.attn_norm = static_cast<const float*>(at(li, ARC_T_ATTN_NORM));
+        L.q = static_cast<const uint8_t*>(at(li, ARC_T_ATTN_Q));
+        L.k = static_cast<const uint8_t*>(at(li, ARC_T_ATTN_K));
+        L.v = static_cast<const uint8_t*>(at(li, ARC_T_ATTN_V));
+        L.qb = static_cast<const float*>(at(li, ARC_T_ATTN_Q_BIAS));
+        L.kb = static_cast<const float*>(at(li, ARC_T_ATTN_K_BIAS));
+        L.vb = static_cast<const float*>(at(li, ARC_T_ATTN_V_BIAS));
+        L.o = static_cast<const uint8_t*>(at(li, ARC_T_ATTN_O));
+        L.ffn_norm = static_cast<const float*>(at(li, ARC_T_FFN_NORM));
+        L.gate = static_cast<const uint8_t*>(at(li, ARC_T_FFN_GATE));
+        L.up = static_cast<const uint8_t*>(at(li, ARC_T_FFN_UP));
+        L.down = static_cast<const uint8_t*>(at(li, ARC_T_FFN_DOWN));
         L.v_type = dims->v_type[l];
         L.down_type = dims->down_type[l];
     }
@@ -687,6 +702,28 @@ int arc_model_destroy(arc_model* m)
 
 uint64_t arc_model_weight_bytes(const arc_model* m) { return m ? m->weight_bytes : 0; }
 
+int arc_model_exec148_reserve(const arc_model* m, void** base, uint64_t* slot_stride, uint32_t* slots)
+{
+    if (!m || !base || !slot_stride || !slots) return set_error(ARC_ERR_INVALID_ARGUMENT, "null argument");
+    *base = m->e148_base;
+    *slot_stride = m->e148_stride;
+    *slots = m->e148_slots;
+    return ARC_OK;
+}
+
+int arc_session_residency(const arc_session* s, arc_residency* out)
+{
+    if (!s || !out) return set_error(ARC_ERR_INVALID_ARGUMENT, "null argument");
+    const arc_model* m = s->model;
+    out->weight_bytes = m->weight_bytes;
+    out->model_arena_bytes = m->arena_bytes;
+    out->exec148_reserve_bytes = m->e148_stride * m->e148_slots;
+    out->kv_bytes = s->kv_bytes;
+    out->working_bytes = s->working_bytes;
+    out->total_bytes = m->arena_bytes + s->kv_bytes + s->working_bytes;
+    return ARC_OK;
+}
+
 int arc_session_create(arc_model* m, uint32_t max_ctx, arc_session** out)
 {
     if (!m || !out || max_ctx == 0) return set_error(ARC_ERR_INVALID_ARGUMENT, "bad session arguments");
@@ -704,55 +741,59 @@ int arc_session_create(arc_model* m, uint32_t max_ctx, arc_session** out)
     const uint32_t KVD = d.kv_heads * kHeadDim, H = d.hidden;
     int rc = check_hip(hipStreamCreateWithFlags(&S->stream, hipStreamNonBlocking), "stream");
     if (rc) return rc;
-    auto alloc = [&](void** p, size_t bytes) {
-        int r = check_hip(hipMalloc(p, bytes), "hipMalloc session");
-        if (!r) S->allocations.push_back(*p);
-        return r;
-    };
-    const uint64_t kv = uint64_t(d.layers) * max_ctx * KVD * sizeof(_Float16);
     S->best_cap = min((d.vocab + 3u) / 4u, 65536u);
-    void* p = nullptr;
-    if ((rc = alloc(&p, kv))) return rc;
-    S->kcache = static_cast<_Float16*>(p);
-    if ((rc = alloc(&p, kv))) return rc;
-    S->vcache = static_cast<_Float16*>(p);
+    const uint64_t kv = uint64_t(d.layers) * max_ctx * KVD * sizeof(_Float16);
     const size_t fl = sizeof(float);
-    if ((rc = alloc(&p, H * fl))) return rc;
-    S->h = static_cast<float*>(p);
-    if ((rc = alloc(&p, H * fl))) return rc;
-    S->h1 = static_cast<float*>(p);
-    if ((rc = alloc(&p, H * fl))) return rc;
-    S->q = static_cast<float*>(p);
-    if ((rc = alloc(&p, H * fl))) return rc;
-    S->attn = static_cast<float*>(p);
-    if ((rc = alloc(&p, size_t(d.ffn) * fl))) return rc;
-    S->s = static_cast<float*>(p);
-    if ((rc = alloc(&p, size_t(d.vocab) * fl))) return rc;
-    S->logits = static_cast<float*>(p);
     const size_t heads_chunks = size_t(d.kv_heads) * kMaxSplits * (d.q_heads / d.kv_heads);
-    if ((rc = alloc(&p, heads_chunks * kHeadDim * fl))) return rc;
-    S->apo = static_cast<float*>(p);
-    if ((rc = alloc(&p, heads_chunks * 2 * fl))) return rc;
-    S->apml = static_cast<float*>(p);
-    if ((rc = alloc(&p, size_t(max_ctx) * 64 * sizeof(float2)))) return rc;
-    S->rope = static_cast<float2*>(p);
-    if ((rc = alloc(&p, size_t(S->best_cap) * sizeof(ArgBest)))) return rc;
-    S->best = static_cast<ArgBest*>(p);
-    if ((rc = alloc(&p, sizeof(DecodeCtl)))) return rc;
-    S->ctl = static_cast<DecodeCtl*>(p);
-    if ((rc = alloc(&p, kCounters * sizeof(uint32_t)))) return rc;
-    S->counters = static_cast<uint32_t*>(p);
+    PrefillBufs& pf = S->pf;
+    pf.part_elems = prefill_part_elems(d);
+    pf.host_slots = (max_ctx + kPfMaxM - 1) / kPfMaxM;
+
+    // The session arena: KV cache, then the decode step's and the prompt
+    // pass's working memory.  Nothing is allocated after this point.
+    ArenaPlan plan;
+    plan.place(&S->kcache, kv);
+    plan.place(&S->vcache, kv);
+    S->kv_bytes = plan.bytes();
+    plan.place(&S->h, H * fl);
+    plan.place(&S->h1, H * fl);
+    plan.place(&S->q, H * fl);
+    plan.place(&S->attn, H * fl);
+    plan.place(&S->s, size_t(d.ffn) * fl);
+    plan.place(&S->logits, size_t(d.vocab) * fl);
+    plan.place(&S->apo, heads_chunks * kHeadDim * fl);
+    plan.place(&S->apml, heads_chunks * 2 * fl);
+    plan.place(&S->rope, size_t(max_ctx) * 64 * sizeof(float2));
+    plan.place(&S->best, size_t(S->best_cap) * sizeof(ArgBest));
+    plan.place(&S->ctl, sizeof(DecodeCtl));
+    plan.place(&S->counters, kCounters * sizeof(uint32_t));
+    plan.place(&S->out_tokens, size_t(S->out_cap) * sizeof(uint32_t));
+    plan.place(&pf.h, size_t(kPfMaxM) * H * fl);
+    plan.place(&pf.x, size_t(kPfMaxM) * H * sizeof(_Float16));
+    plan.place(&pf.xs, size_t(kPfMaxM) * d.ffn * sizeof(_Float16));
+    plan.place(&pf.q, size_t(kPfMaxM) * H * fl);
+    plan.place(&pf.part, pf.part_elems * fl);
+    plan.place(&pf.tokens, kPfMaxM * sizeof(uint32_t));
+    plan.pad(4096);  // nothing near the allocation's end is read past it
+    S->working_bytes = plan.bytes() - S->kv_bytes;
+    if ((rc = plan.commit(&S->arena, "session arena"))) return rc;
+
+    // Pinned host staging, one allocation: control-block uploads (slot 0 the
+    // download), generated tokens, prompt tokens per pass.
+    const size_t ctl_bytes = (size_t(max_ctx) + 1) * sizeof(DecodeCtl);
+    const size_t tok_bytes = size_t(S->out_cap) * sizeof(uint32_t);
+    const size_t prompt_bytes = size_t(pf.host_slots) * kPfMaxM * sizeof(uint32_t);
+    if ((rc = check_hip(hipHostMalloc(&S->pinned, ctl_bytes + tok_bytes + prompt_bytes, hipHostMallocDefault),
+                        "pinned staging")))
+        return rc;
+    S->host_ctl = static_cast<DecodeCtl*>(S->pinned);
+    S->host_tokens = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(S->pinned) + ctl_bytes);
+    pf.host_tokens = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(S->pinned) + ctl_bytes + tok_bytes);
+
     if ((rc = check_hip(hipMemset(S->counters, 0, kCounters * sizeof(uint32_t)), "counters"))) return rc;
-    if ((rc = alloc(&p, size_t(S->out_cap) * sizeof(uint32_t)))) return rc;
-    S->out_tokens = static_cast<uint32_t*>(p);
-    if ((rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&S->host_ctl), (size_t(max_ctx) + 1) * sizeof(DecodeCtl),
-                                      hipHostMallocDefault),
-                        "pinned ctl")))
-        return rc;
-    if ((rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&S->host_tokens), size_t(S->out_cap) * sizeof(uint32_t),
-                                      hipHostMallocDefault),
-                        "pinned tokens")))
-        return rc;
+    // rows past a prompt are read (never written) by the prompt-pass GEMM tiles
+    if ((rc = check_hip(hipMemset(pf.x, 0, size_t(kPfMaxM) * H * sizeof(_Float16)), "prefill x"))) return rc;
+    if ((rc = check_hip(hipMemset(pf.xs, 0, size_t(kPfMaxM) * d.ffn * sizeof(_Float16)), "prefill xs"))) return rc;
     {   // RoPE factors: angle = pos * theta^(-2p/128) in fp64, cos and sin rounded to fp32
         double inv[64];
         for (int i = 0; i < 64; ++i) inv[i] = std::pow(double(d.rope_theta), -2.0 * double(i) / double(kHeadDim));

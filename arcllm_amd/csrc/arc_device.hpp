@@ -20,6 +20,14 @@ constexpr int kE148Bytes = 148;
 // Defined in arc_runtime.cpp.
 int set_error(int code, const char* fmt, ...);
 int check_hip(hipError_t e, const char* what);
+// The library's one hipMalloc call site (counted, see arc_device_allocations).
+int device_alloc(void** ptr, size_t bytes, const char* what);
+// Device memory a planned arena must leave free for the runtime itself
+// (code objects, graph kernel arguments, library workspaces).
+constexpr uint64_t kResidencyHeadroom = 512ull << 20;
+// ARC_OK when `bytes` more fit in the free device memory with the headroom
+// to spare; otherwise ARC_ERR_OUT_OF_MEMORY naming `what`.
+int residency_fits(uint64_t bytes, const char* what);
 
 // Decode-step control block in device memory: the graph of one decode step
 // reads the position and token from here, and the argmax writes them back.

@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 
 namespace arc {
 
@@ -135,11 +136,39 @@ __global__ __launch_bounds__(256) void k_exec148_validate(const uint8_t* __restr
     if (threadIdx.x == 0 && n) atomicAdd(mismatched, static_cast<unsigned long long>(n));
 }
 
+// The validation's mismatch counter: one per device, in static device memory,
+// so a validation allocates nothing.  Calls hold g_count_mu from clearing it
+// to reading it back (validation is synchronous), so they never share it.
+static __device__ __align__(256) unsigned long long g_mismatch_count;
+
 }  // namespace arc
 
 using namespace arc;
 
 namespace {
+
+constexpr int kMaxCountDevices = 64;
+std::mutex g_count_mu;
+unsigned long long* g_count_ptr[kMaxCountDevices];
+
+// Device address of g_mismatch_count on the current device (looked up once
+// per device with it current).  Call with g_count_mu held.
+int mismatch_counter(unsigned long long** out)
+{
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "current device");
+    if (rc) return rc;
+    if (dev < 0 || dev >= kMaxCountDevices) return set_error(ARC_ERR_UNSUPPORTED, "device %d out of range", dev);
+    if (!g_count_ptr[dev]) {
+        void* ptr = nullptr;
+        if ((rc = check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_mismatch_count)), "validate counter address")))
+            return rc;
+        if (!ptr) return set_error(ARC_ERR_DEVICE, "no device address for the validate counter");
+        g_count_ptr[dev] = static_cast<unsigned long long*>(ptr);
+    }
+    *out = g_count_ptr[dev];
+    return ARC_OK;
+}
 
 int check_e148(const void* q4, uint32_t rows, uint32_t K, const void* exec, uint64_t& nblocks)
 {
@@ -181,8 +210,9 @@ int arc_exec148_validate_many(const void* const* q4, const void* const* exec, ui
         if (rc) return rc;
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
+    std::lock_guard<std::mutex> lock(g_count_mu);
     unsigned long long* cnt = nullptr;
-    int rc = check_hip(hipMalloc(reinterpret_cast<void**>(&cnt), sizeof(*cnt)), "exec148 validate counter");
+    int rc = mismatch_counter(&cnt);
     if (rc) return rc;
     unsigned long long host = 0;
     rc = check_hip(hipMemcpyAsync(cnt, &host, sizeof(host), hipMemcpyHostToDevice, s), "exec148 validate clear");
@@ -193,8 +223,9 @@ int arc_exec148_validate_many(const void* const* q4, const void* const* exec, ui
         rc = check_hip(hipGetLastError(), "exec148 validate");
     }
     if (!rc) rc = check_hip(hipMemcpyAsync(&host, cnt, sizeof(host), hipMemcpyDeviceToHost, s), "exec148 validate result");
-    if (!rc) rc = check_hip(hipStreamSynchronize(s), "exec148 validate sync");
-    (void)hipFree(cnt);
+    // on an error the wait still runs, so no launch outlives the lock
+    const int sync = check_hip(hipStreamSynchronize(s), "exec148 validate sync");
+    if (!rc) rc = sync;
     if (!rc) *mismatched = host;
     return rc;
 }

@@ -37,31 +37,8 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // native vector: stays in registers
 
-constexpr int kPfMaxM = 256;       // prompt rows per pass
 constexpr int kPfKT = 128;         // K columns per LDS stage (half a super-block)
 constexpr int kPfLd = kPfKT + 8;   // padded LDS row, in halves
-
-struct PrefillBufs {
-    float* h = nullptr;         // [256][hidden] residual stream
-    _Float16* x = nullptr;      // [256][hidden] fp16 GEMM input (normed h, attention output)
-    _Float16* xs = nullptr;     // [256][ffn] fp16 SwiGLU output (input of ffn_down)
-    float* q = nullptr;         // [256][hidden] q after RoPE
-    float* part = nullptr;      // split-K partials
-    size_t part_elems = 0;
-    uint32_t* tokens = nullptr; // [256] device
-    uint32_t* host_tokens = nullptr;  // pinned staging, one slot of 256 per pass of a call
-    uint32_t host_slots = 0;
-    uint32_t kernels = 0;       // launches of the last prompt pass
-    std::vector<void*> allocs;
-};
-
-void destroy_prefill(PrefillBufs* pf)
-{
-    if (!pf) return;
-    for (void* p : pf->allocs) (void)hipFree(p);
-    if (pf->host_tokens) (void)hipHostFree(pf->host_tokens);
-    delete pf;
-}
 
 // ------------------------------------------------------------------ GEMM
 struct PfGemm {
@@ -922,72 +899,35 @@ void launch_attn(uint32_t hpk, dim3 grid, hipStream_t st, const float* q, const 
     }
 }
 
-int ensure_bufs(arc_session* S)
-{
-    if (S->pf) return ARC_OK;
-    const arc_model_dims& d = S->model->dims;
-    std::unique_ptr<PrefillBufs> pf(new (std::nothrow) PrefillBufs);
-    if (!pf) return set_error(ARC_ERR_OUT_OF_MEMORY, "host allocation");
-    auto alloc = [&](void** p, size_t bytes) {
-        const int r = check_hip(hipMalloc(p, bytes), "hipMalloc prefill");
-        if (!r) pf->allocs.push_back(*p);
-        return r;
-    };
-    const uint32_t kvd = d.kv_heads * kHeadDim;
-    size_t part = 0;
-    {   // q|k|v (one launch), o, down: [split][256][columns] partials
-        uint32_t gx, sp, bps;
-        const uint32_t qkv_cols = ((d.hidden + kvd + 127) / 128 + (kvd + 127) / 128) * 128;
-        split_plan(qkv_cols, d.hidden / kQK, gx, sp, bps);
-        part = std::max(part, size_t(sp) * kPfMaxM * (d.hidden + 2 * kvd));
-        split_plan(d.hidden, d.hidden / kQK, gx, sp, bps);
-        part = std::max(part, size_t(sp) * kPfMaxM * d.hidden);
-        split_plan(d.hidden, d.ffn / kQK, gx, sp, bps);
-        part = std::max(part, size_t(sp) * kPfMaxM * d.hidden);
-    }
-    void* p = nullptr;
-    int rc;
-    if ((rc = alloc(&p, size_t(kPfMaxM) * d.hidden * sizeof(float)))) return rc;
-    pf->h = static_cast<float*>(p);
-    if ((rc = alloc(&p, size_t(kPfMaxM) * d.hidden * sizeof(_Float16)))) return rc;
-    pf->x = static_cast<_Float16*>(p);
-    if ((rc = alloc(&p, size_t(kPfMaxM) * d.ffn * sizeof(_Float16)))) return rc;
-    pf->xs = static_cast<_Float16*>(p);
-    if ((rc = alloc(&p, size_t(kPfMaxM) * d.hidden * sizeof(float)))) return rc;
-    pf->q = static_cast<float*>(p);
-    if ((rc = alloc(&p, part * sizeof(float)))) return rc;
-    pf->part = static_cast<float*>(p);
-    pf->part_elems = part;
-    if ((rc = alloc(&p, kPfMaxM * sizeof(uint32_t)))) return rc;
-    pf->tokens = static_cast<uint32_t*>(p);
-    // rows past the prompt are read (never written) by the GEMM tiles
-    if ((rc = check_hip(hipMemset(pf->x, 0, size_t(kPfMaxM) * d.hidden * sizeof(_Float16)), "prefill x"))) return rc;
-    if ((rc = check_hip(hipMemset(pf->xs, 0, size_t(kPfMaxM) * d.ffn * sizeof(_Float16)), "prefill xs"))) return rc;
-    S->pf = pf.release();
-    return ARC_OK;
-}
-
 }  // namespace
+
+uint64_t prefill_part_elems(const arc_model_dims& d)
+{
+    // q|k|v (one launch), o, down: [split][256][columns] partials
+    const uint32_t kvd = d.kv_heads * kHeadDim;
+    uint32_t gx, sp, bps;
+    uint64_t part = 0;
+    const uint32_t qkv_cols = ((d.hidden + kvd + 127) / 128 + (kvd + 127) / 128) * 128;
+    split_plan(qkv_cols, d.hidden / kQK, gx, sp, bps);
+    part = std::max(part, uint64_t(sp) * kPfMaxM * (d.hidden + 2 * kvd));
+    split_plan(d.hidden, d.hidden / kQK, gx, sp, bps);
+    part = std::max(part, uint64_t(sp) * kPfMaxM * d.hidden);
+    split_plan(d.hidden, d.ffn / kQK, gx, sp, bps);
+    part = std::max(part, uint64_t(sp) * kPfMaxM * d.hidden);
+    return part;
+}
 
 int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos0, bool logits)
 {
-    int rc = ensure_bufs(S);
-    if (rc) return rc;
-    PrefillBufs* pf = S->pf;
+    int rc = ARC_OK;
+    PrefillBufs* pf = &S->pf;
     const arc_model* Mdl = S->model;
     const arc_model_dims& d = Mdl->dims;
     const uint32_t H = d.hidden, F = d.ffn, kvd = d.kv_heads * kHeadDim, hpk = d.q_heads / d.kv_heads;
     const uint32_t passes = (n + kPfMaxM - 1) / kPfMaxM;
-    if (pf->host_slots < passes) {
-        if (pf->host_tokens) (void)hipHostFree(pf->host_tokens);
-        pf->host_tokens = nullptr;
-        pf->host_slots = 0;
-        if ((rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&pf->host_tokens),
-                                          size_t(passes) * kPfMaxM * sizeof(uint32_t), hipHostMallocDefault),
-                            "pinned prompt")))
-            return rc;
-        pf->host_slots = passes;
-    }
+    if (passes > pf->host_slots)  // the caller keeps pos0 + n within max_ctx
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "prompt of %u tokens exceeds the session's %u positions", n,
+                         S->max_ctx);
     hipStream_t st = S->stream;
     uint32_t nk = 0;
     auto chk = [&](hipError_t e, const char* what) {
@@ -1102,7 +1042,6 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             nk += 1;
         }
     }
-    pf->kernels = nk;
     S->prefill_kernels = nk;
     return ARC_OK;
 }

@@ -4,14 +4,20 @@
 // reference (VkRuntime::{init,make_buffer,destroy_buffer},
 // src/arcllm_v1_vulkan_runtime_support.h:498-664).
 #include "../../include/arcllm_hip.h"
+#include "arc_device.hpp"
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 
 namespace arc {
+
+// Every device allocation of the library goes through device_alloc: the
+// model arena, the session arena and arc_malloc.
+static std::atomic<uint64_t> g_device_allocs{0};
 
 static thread_local char g_err[512] = "";
 
@@ -31,6 +37,28 @@ int check_hip(hipError_t e, const char* what)
                      : (e == hipErrorNoDevice || e == hipErrorInvalidDevice) ? ARC_ERR_NO_DEVICE
                                                                                : ARC_ERR_DEVICE;
     return set_error(code, "%s: %s (%d)", what, hipGetErrorString(e), int(e));
+}
+
+int device_alloc(void** ptr, size_t bytes, const char* what)
+{
+    *ptr = nullptr;
+    const int rc = check_hip(hipMalloc(ptr, bytes), what);
+    if (!rc) g_device_allocs.fetch_add(1, std::memory_order_relaxed);
+    return rc;
+}
+
+int residency_fits(uint64_t bytes, const char* what)
+{
+    size_t free_b = 0, total_b = 0;
+    const int rc = check_hip(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
+    if (rc) return rc;
+    if (bytes > uint64_t(free_b) || uint64_t(free_b) - bytes < kResidencyHeadroom)
+        return set_error(ARC_ERR_OUT_OF_MEMORY,
+                         "%s: planned residency %llu bytes exceeds the free device memory %llu bytes less the "
+                         "%llu-byte headroom",
+                         what, static_cast<unsigned long long>(bytes), static_cast<unsigned long long>(free_b),
+                         static_cast<unsigned long long>(kResidencyHeadroom));
+    return ARC_OK;
 }
 
 }  // namespace arc
@@ -77,8 +105,14 @@ int arc_device_info(char* name, size_t name_len, char* arch, size_t arch_len)
 int arc_malloc(void** ptr, size_t bytes)
 {
     if (!ptr || bytes == 0) return set_error(ARC_ERR_INVALID_ARGUMENT, "bad malloc arguments");
-    *ptr = nullptr;
-    return check_hip(hipMalloc(ptr, bytes), "hipMalloc");
+    return arc::device_alloc(ptr, bytes, "hipMalloc");
+}
+
+int arc_device_allocations(uint64_t* count)
+{
+    if (!count) return set_error(ARC_ERR_INVALID_ARGUMENT, "null count");
+    *count = arc::g_device_allocs.load(std::memory_order_relaxed);
+    return ARC_OK;
 }
 
 int arc_free(void* ptr) { return ptr ? check_hip(hipFree(ptr), "hipFree") : ARC_OK; }

@@ -20,7 +20,6 @@ namespace {
 constexpr std::uint32_t kQK = 256;          // elements per block
 constexpr std::uint32_t kQ4Block = 144;     // Q4_K block bytes
 constexpr std::uint32_t kE148Block = 148;   // EXEC148 block bytes
-constexpr std::uint64_t kSlotAlign = 256;   // device offset alignment of a layer image
 
 // One Q4_K block -> one EXEC148 block: d and dmin bytes as they are, the
 // eight 6-bit (scale, min) pairs unpacked to a byte each, then the 256 codes
@@ -146,15 +145,13 @@ HipQ4DownBackend::HipQ4DownBackend(arc_model* model, std::vector<std::uint32_t> 
       sidecar_(std::move(sidecar))
 {
     layer_bytes_ = exec148_bytes(rows_, K_);
-    slot_stride_ = (layer_bytes_ + kSlotAlign - 1) / kSlotAlign * kSlotAlign;
     family_bytes_ = layer_bytes_ * layers_.size();
+    void* base = nullptr;
+    if (arc_model_exec148_reserve(model_, &base, &slot_stride_, &reserve_slots_) == ARC_OK)
+        reserve_ = static_cast<std::uint8_t*>(base);
 }
 
-HipQ4DownBackend::~HipQ4DownBackend()
-{
-    (void)unroute();
-    if (exec_) (void)arc_free(exec_);
-}
+HipQ4DownBackend::~HipQ4DownBackend() { (void)unroute(); }
 
 bool HipQ4DownBackend::p3_available() const noexcept
 {
@@ -166,10 +163,9 @@ bool HipQ4DownBackend::p3_available() const noexcept
     }
 }
 
-// Frees the image and resets the state after a failed acquisition.
+// Gives the reserve up and resets the state after a failed acquisition.
 void HipQ4DownBackend::drop() noexcept
 {
-    if (exec_) (void)arc_free(exec_);
     exec_ = nullptr;
     resident_ = false;
     validated_ = false;
@@ -244,12 +240,12 @@ bind::BackendStatus HipQ4DownBackend::acquire(reg::AcquisitionPathId path, reg::
     if (path != q4reg::kAcquirePrimary && path != q4reg::kAcquireSecondary && path != q4reg::kAcquireTertiary)
         return bind::BackendStatus::UNAVAILABLE;
     try {
-        void* p = nullptr;
-        if (arc_malloc(&p, slot_stride_ * layers_.size()) != ARC_OK) {
-            last_error_ = arc_last_error();
+        // the model's reserve holds one slot per Q4_K ffn_down, in layer order
+        if (!reserve_ || reserve_slots_ < layers_.size() || slot_stride_ < layer_bytes_) {
+            last_error_ = "the model has no EXEC148 reserve for these layers";
             return bind::BackendStatus::ACQUISITION_FAILED;
         }
-        exec_ = static_cast<std::uint8_t*>(p);
+        exec_ = reserve_;
         ++counters_.b_allocations;
         bool ok;
         if (path == q4reg::kAcquirePrimary) {
@@ -328,10 +324,6 @@ bind::BackendStatus HipQ4DownBackend::release(reg::PrimitiveId target, bind::Rep
         return bind::BackendStatus::INVALID_BINDING_STATE;
     // a session must not keep a route into freed memory
     if (!unroute()) return bind::BackendStatus::RELEASE_FAILED;
-    if (arc_free(exec_) != ARC_OK) {
-        last_error_ = arc_last_error();
-        return bind::BackendStatus::RELEASE_FAILED;
-    }
     exec_ = nullptr;
     resident_ = false;
     validated_ = false;

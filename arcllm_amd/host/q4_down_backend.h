@@ -14,7 +14,10 @@
 //   P0 (kAcquireTertiary):  repacked on the host from the GGUF payload and
 //                           uploaded;
 // validated block by block against the Q4_K source on the GPU
-// (arc_exec148_validate), and released on eviction.  The shape of this class
+// (arc_exec148_validate), and released on eviction.  The image lives in the
+// model's EXEC148 reserve (arc_model_exec148_reserve), planned with the
+// model's arena: acquiring fills it and releasing gives it up, and neither
+// allocates or frees device memory.  The shape of this class
 // follows the reference's Q4VulkanBackendV4
 // (src/arcllm_v1_q4_vulkan_backend_v4_runtime.h:196-420): same statuses for
 // the same conditions, same counters, one representation with handle 1,
@@ -127,9 +130,11 @@ private:
     std::uint32_t rows_, K_;
     std::string sidecar_;
     std::uint64_t layer_bytes_ = 0;   // one layer's image
-    std::uint64_t slot_stride_ = 0;   // its offset step on the device (256-byte aligned)
+    std::uint64_t slot_stride_ = 0;   // its offset step in the model's EXEC148 reserve
     std::uint64_t family_bytes_ = 0;  // layers x layer_bytes (the residency and sidecar size)
-    std::uint8_t* exec_ = nullptr;    // device image
+    std::uint8_t* reserve_ = nullptr; // the model's EXEC148 reserve (null: none)
+    std::uint32_t reserve_slots_ = 0;
+    std::uint8_t* exec_ = nullptr;    // device image while resident (= reserve_)
     arc_session* routed_ = nullptr;   // session currently routed to the image
     bool resident_ = false;
     bool validated_ = false;

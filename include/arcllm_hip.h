@@ -66,6 +66,11 @@ int arc_device_info(char *name, size_t name_len, char *arch, size_t arch_len);
 
 int arc_malloc(void **ptr, size_t bytes);
 int arc_free(void *ptr);
+/* Device allocations the library has made in this process (model and
+ * session arenas, arc_malloc).  No counterpart in the reference: lets a
+ * caller check that decoding, the prompt pass and route changes allocate
+ * nothing once a session exists. */
+int arc_device_allocations(uint64_t *count);
 int arc_memcpy_htod(void *dst, const void *src, size_t bytes, arc_stream_t stream);
 int arc_memcpy_dtoh(void *dst, const void *src, size_t bytes, arc_stream_t stream);
 int arc_memcpy_dtod(void *dst, const void *src, size_t bytes, arc_stream_t stream);
@@ -251,12 +256,38 @@ int arc_model_create(const arc_model_dims *dims, const void *const *tensors, arc
 int arc_model_create_synthetic(const arc_model_dims *dims, uint64_t seed, arc_model **out);
 int arc_model_destroy(arc_model *model);
 uint64_t arc_model_weight_bytes(const arc_model *model);
+/* A model is one device allocation (its arena): every tensor at a 256-byte
+ * aligned offset in slot order, then, when some ffn_down is Q4_K, a reserve
+ * for the EXEC148 image of every Q4_K ffn_down (slot i = the i-th such layer
+ * in layer order, at base + i * slot_stride).  The Q4_K FFN-down backend
+ * builds its representation there instead of allocating at acquisition
+ * (the reference allocates it then, src/arcllm_v1_q4_vulkan_backend_v4_runtime.h:238).
+ * slots = 0 and base = NULL when no ffn_down is Q4_K. */
+int arc_model_exec148_reserve(const arc_model *model, void **base, uint64_t *slot_stride, uint32_t *slots);
 
 /* A decode session: fp16 KV cache [layer][max_ctx][kv_heads*128] for K and
  * V (GPU-resident across steps), working buffers and the captured step.
  * max_ctx is 1..32768 (ARC_ERR_UNSUPPORTED above). */
 int arc_session_create(arc_model *model, uint32_t max_ctx, arc_session **out);
 int arc_session_destroy(arc_session *session);
+
+/* Residency plan of a session and its model, in bytes: the reference's
+ * weight / KV / working accounting and its budget check
+ * (src/arcllm_v1_runtime.cpp:227-266).  A session is one device allocation
+ * (the KV cache, then the decode step's and the prompt pass's working
+ * memory) planned in full at arc_session_create; nothing is allocated on the
+ * device after that.  arc_model_create and arc_session_create each refuse,
+ * with ARC_ERR_OUT_OF_MEMORY, a plan that does not fit the free device
+ * memory less a 512 MiB headroom. */
+typedef struct arc_residency {
+    uint64_t weight_bytes;          /* tensor bytes of the model */
+    uint64_t model_arena_bytes;     /* the model's allocation: tensors, alignment, EXEC148 reserve */
+    uint64_t exec148_reserve_bytes; /* of which the EXEC148 reserve */
+    uint64_t kv_bytes;              /* fp16 K and V cache */
+    uint64_t working_bytes;         /* the rest of the session's allocation */
+    uint64_t total_bytes;           /* model arena + kv + working */
+} arc_residency;
+int arc_session_residency(const arc_session *session, arc_residency *out);
 /* Device pointers of one layer's K and V cache. */
 int arc_session_kv(arc_session *session, uint32_t layer, void **k, void **v);
 /* Positions [0, ctx) of every layer's K and V := fp16(N(0, 1)), drawn from

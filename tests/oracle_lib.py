@@ -268,6 +268,26 @@ class DecodeOracle:
         assert rc == 0
         return logits
 
+    def follow(self, token, pos, gpu_tokens, tie=2e-3):
+        """Teacher-forced check of a GPU greedy run, every step compared: step
+        i feeds `token` (i = 0) or the GPU's token i - 1 at position pos + i,
+        and the GPU's token i must be the oracle's argmax, or its runner-up
+        when the top-2 margin is below tie * max|logit| (a near tie, where
+        fp32 and fp64 may order the two differently).  Returns the number of
+        near-tie steps the GPU took the runner-up at."""
+        ties = 0
+        for i, g in enumerate(np.asarray(gpu_tokens).tolist()):
+            lg = self.step(int(token), pos + i)
+            order = np.argsort(-lg, kind="stable")
+            if g != int(order[0]):
+                margin, scale = float(lg[order[0]] - lg[order[1]]), float(np.max(np.abs(lg)))
+                assert g == int(order[1]) and margin < tie * scale, (
+                    f"step {i}: gpu token {g}, oracle {int(order[0])} / {int(order[1])}, margin {margin:.4g} "
+                    f"(near-tie bound {tie * scale:.4g})")
+                ties += 1
+            token = g
+        return ties
+
     def greedy(self, token, pos, n, log=None):
         """n greedy steps from `token` at `pos`.  Returns (tokens, runner-up
         tokens, top1-top2 margins, max|logit| per step); `log` gets one line

@@ -34,6 +34,22 @@ def test_library_exports_every_declared_symbol():
     assert set(arc.EXPORTED) <= syms | {"arc_tune_force"}
 
 
+def test_device_memory_is_allocated_in_one_place():
+    """hipMalloc is called only by device_alloc (arc_runtime.cpp), which the
+    model arena, the session arena and arc_malloc go through; no kernel
+    source or host file allocates device memory by itself."""
+    calls = {}
+    for path in glob.glob(os.path.join(ROOT, "arcllm_amd", "csrc", "*")) + \
+            glob.glob(os.path.join(ROOT, "arcllm_amd", "host", "**", "*"), recursive=True):
+        if not os.path.isfile(path):
+            continue
+        text = re.sub(r"//.*", "", open(path).read())
+        for name in ("hipMalloc(", "hipMallocAsync(", "hipExtMallocWithFlags(", "hipMallocManaged(", "arc_malloc("):
+            if name in text:
+                calls.setdefault(os.path.basename(path), []).append(name)
+    assert calls == {"arc_runtime.cpp": ["hipMalloc(", "arc_malloc("]}, calls
+
+
 def test_version_and_device_count_without_gpu_is_not_an_error():
     assert b"gfx950" in arc.lib().arc_version()
     assert arc.device_count() >= 0

@@ -29,29 +29,25 @@ def _log(msg):
     sys.stdout.flush()
 
 
-def oracle_generate(d, T, prompt, max_new):
-    # prompts of two or more tokens take the batched pass (fp16 GEMM operands):
-    # the oracle follows it with its fp16-operand mode, then decodes exactly
-    o = orc.DecodeOracle(d, T, len(prompt) + max_new, f16_operands=len(prompt) > 1)
+def oracle_follow(d, T, prompt, gpu_tokens):
+    """Every generated token checked against the oracle, teacher-forced: the
+    prompt through the oracle (fp16-operand mode when it has two or more
+    tokens, like the batched prompt pass), the first token against its argmax
+    (runner-up allowed below the prompt pass's near-tie bound, 2e-2 of
+    max|logit|), then each later token against the exact oracle fed the GPU's
+    previous token (DecodeOracle.follow).  Returns the near-tie steps."""
+    gpu_tokens = np.asarray(gpu_tokens)
+    o = orc.DecodeOracle(d, T, len(prompt) + len(gpu_tokens), f16_operands=len(prompt) > 1)
     for i, t in enumerate(prompt):
         lg = o.step(int(t), i)
     o.f16 = 0
     order = np.argsort(-lg, kind="stable")
-    first, second0 = int(order[0]), int(order[1])
-    m0, s0 = float(lg[order[0]] - lg[order[1]]), float(np.max(np.abs(lg)))
-    toks, second, margins, scale = o.greedy(first, len(prompt), max_new - 1)
-    return (np.concatenate([[first], toks]).astype(np.uint32), np.concatenate([[second0], second]),
-            np.concatenate([[m0], margins]), np.concatenate([[s0], scale]))
-
-
-def tokens_match(gpu, ref, second, margins, scale):
-    diff = np.nonzero(np.asarray(gpu) != ref)[0]
-    if diff.size == 0:
-        return len(gpu)
-    i = int(diff[0])
-    _log(f"first differing step {i}: gpu={gpu[i]} oracle={ref[i]} margin={margins[i]:.4g}")
-    assert margins[i] < 2e-3 * scale[i] and gpu[i] == second[i], "token differs at a step that is not a near tie"
-    return i
+    ties = 0
+    if int(gpu_tokens[0]) != int(order[0]):
+        margin, scale = float(lg[order[0]] - lg[order[1]]), float(np.max(np.abs(lg)))
+        assert int(gpu_tokens[0]) == int(order[1]) and margin < 2e-2 * scale, "first token is not a near tie"
+        ties = 1
+    return ties + o.follow(int(gpu_tokens[0]), len(prompt), gpu_tokens[1:])
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -79,10 +75,9 @@ def test_generate_cli_matches_oracle(tmp_path):
     res = json.loads(r.stdout)
     assert res["schema"] == "arcllm.v1.runtime.result.v0.1"
     gpu = res["generated_token_ids"]
-    ref, second, margins, scale = oracle_generate(d, T, prompt, max_new)
-    _log(f"gpu={gpu}\nref={ref.tolist()}\nmin margin={margins.min():.4g}")
+    _log(f"gpu={gpu}")
     assert len(gpu) == max_new
-    assert tokens_match(gpu, ref, second, margins, scale) >= max_new // 2
+    _log(f"near-tie steps: {oracle_follow(d, T, prompt, gpu)}")
     st = res["stats"]
     per_step = 1 + 5 * d.layers
     # batched prompt pass: embed + first norm, 8 launches per layer, LM head + next token
@@ -126,7 +121,6 @@ def test_generate_routes_by_scope_and_reuse(tmp_path):
     th = thresholds()
     t0, t1 = th["profile0"]["p1"], th["profile1"]["p1"]
     longest = t1 + 2
-    ref, second, margins, scale = oracle_generate(d, T, prompt, longest)
     cases = [  # (max_new, profile, scope, route B expected)
         (longest, 0, 0, False), (t0, 0, 1, False), (t0 + 1, 0, 1, True), (t1, 1, 1, False), (t1 + 1, 1, 1, True)]
     for max_new, prof, scope, route_b in cases:
@@ -141,7 +135,8 @@ def test_generate_routes_by_scope_and_reuse(tmp_path):
         else:
             assert (st["route_a_steps"], st["route_b_steps"]) == (steps, 0)
             assert (st["acquire_events"], st["evict_events"], st["b_allocations"]) == (0, 0, 0)
-        assert tokens_match(res["generated_token_ids"], ref[:max_new], second, margins, scale) >= max_new // 2
+        assert len(res["generated_token_ids"]) == max_new
+        _log(f"near-tie steps: {oracle_follow(d, T, prompt, res['generated_token_ids'])}")
 
 
 def test_q4_paths_tool_all_acquisition_paths(tmp_path):
@@ -172,10 +167,10 @@ def test_q4_paths_tool_all_acquisition_paths(tmp_path):
     assert res["images_equal"] is True
     assert os.path.getsize(sidecar) == image.size
     o = orc.DecodeOracle(d, T, ctx + steps + 2)
-    o.fill_kv(ctx, kv_seed, arc.synth_normal)
-    ref, second, margins, scale = o.greedy(1234, ctx, steps)
     for route in ("route_a", "route_b"):
-        assert tokens_match(res[route]["tokens"], ref, second, margins, scale) >= steps // 2, route
+        assert len(res[route]["tokens"]) == steps
+        o.fill_kv(ctx, kv_seed, arc.synth_normal)
+        _log(f"{route}: near-tie steps {o.follow(1234, ctx, res[route]['tokens'])}")
 
 
 def test_generate_single_token_request(tmp_path):
@@ -188,8 +183,8 @@ def test_generate_single_token_request(tmp_path):
                        timeout=120)
     assert r.returncode == 0, r.stderr
     res = json.loads(r.stdout)
-    ref, *_ = oracle_generate(d, T, [3], 1)
-    assert res["generated_token_ids"] == [int(ref[0])]
+    assert len(res["generated_token_ids"]) == 1
+    oracle_follow(d, T, [3], res["generated_token_ids"])
     assert res["stats"]["decode_steps"] == 0 and res["stats"]["decode_dispatches_per_step"] == 0
 
 
