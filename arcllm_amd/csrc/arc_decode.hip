@@ -63,6 +63,11 @@ __device__ __host__ inline AttnSplit attn_split(uint32_t T)
 constexpr int kKtStride = kChunk + 1;
 constexpr int kStageWords = (kHeadDim / 2) * kKtStride + kChunk * (kHeadDim / 2);
 constexpr int kAttnThreads = 512;  // 8 waves: wave w computes query head w of the group
+static_assert(kMaxSplits <= kWave, "the merge takes one split per lane");
+#ifndef ARC_ATTN_MERGE_BATCH
+#define ARC_ATTN_MERGE_BATCH 16
+#endif
+constexpr int kAttnMergeBatch = ARC_ATTN_MERGE_BATCH;  // split outputs loaded per batch in the merge
 // The scores' softmax weights (one kChunk row per head wave), reused by the
 // merge for the split weights ([kMaxSplits][HPK]).
 template <int HPK>
@@ -84,7 +89,7 @@ constexpr int attn_ew_words()
 // (max, sum, o).  A single split writes the output; otherwise each split's
 // (m, l, o) goes to memory past the L2 (st_agent) and the last workgroup of
 // kv head g to arrive merges the splits in split order: M = max m_s,
-// f_s = e^(m_s - M), L = sum l_s f_s, out = sum o_s f_s / L.  Every
+// f_s = e^(m_s - M), L = sum l_s f_s, out = sum o_s (f_s / L).  Every
 // reduction has a fixed order, so the result does not depend on which
 // workgroup arrives last.
 // Semantics: src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1177-1212,
@@ -96,9 +101,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
     auto stage = [&](uint32_t i) { return smw + (i & 1u) * kStageWords; };
     float* qs = reinterpret_cast<float*>(smw + 2 * kStageWords);  // [HPK][128]
     float* ew = qs + HPK * kHeadDim;                               // [HPK waves][kChunk]; merge: [kMaxSplits][HPK]
-    float* mm = ew + attn_ew_words<HPK>();                          // [kMaxSplits][HPK] (+ [HPK])
-    float* ll = mm + kMaxSplits * HPK + HPK;                       // [kMaxSplits][HPK]
-    uint32_t* flag = reinterpret_cast<uint32_t*>(ll + kMaxSplits * HPK);
+    uint32_t* flag = reinterpret_cast<uint32_t*>(ew + attn_ew_words<HPK>());
 
     const uint32_t s = blockIdx.x, g = blockIdx.y;
     const uint32_t kvd = a.kv_heads * kHeadDim;
@@ -214,39 +217,31 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
     }
     if (!arrive_last(a.counter + g, sp.nsplit, flag)) return;
 
-    // merge (last workgroup of kv head g): thread -> (head hh, dims 2dp, 2dp+1);
-    // the splits' o in batches of 16, the first batch issued before the
-    // split weights are known
-    float* fw = ew;                      // [kMaxSplits][HPK] split weights (ew is free now)
-    float* Mh = mm + kMaxSplits * HPK;   // [HPK] (past mm; ll follows at its own offset)
+    // merge (last workgroup of kv head g).  Wave h, lane = split: the split
+    // weights w_s = e^(m_s - M) / L of head h (M and L by wave reductions)
+    // into LDS; then thread -> (head hh, dims 2dp, 2dp+1) sums the splits' o
+    // weighted, in split order, loads in batches of kB (the first batch is
+    // issued before the weights are known).
+    float* fw = ew;  // [kMaxSplits][HPK] split weights (ew is free now)
     const bool owner = uint32_t(tid) < HPK * (kHeadDim / 2);
     const uint32_t hh = uint32_t(tid) / (kHeadDim / 2), dp = uint32_t(tid) % (kHeadDim / 2);
-    const float* src = a.po + (base * HPK + hh) * kHeadDim + 2 * dp;
-    constexpr int kB = 16;
+    const float* src = a.po + (base * HPK + min(hh, uint32_t(HPK - 1))) * kHeadDim + 2 * dp;
+    constexpr int kB = kAttnMergeBatch;
     float2 ov[kB];
     if (owner)
 #pragma unroll
         for (int u = 0; u < kB; ++u) ov[u] = ld_agent2(src + uint64_t(min(uint32_t(u), sp.nsplit - 1)) * HPK * kHeadDim);
-    if (uint32_t(tid) < sp.nsplit * HPK) {
-        const uint32_t ss = uint32_t(tid) / HPK, h2 = uint32_t(tid) - ss * HPK;
-        const float2 ml = ld_agent2(a.pml + ((base + ss) * HPK + h2) * 2);
-        mm[ss * HPK + h2] = ml.x;
-        ll[ss * HPK + h2] = ml.y;
+    if (h < HPK) {
+        const bool in = uint32_t(lane) < sp.nsplit;
+        const uint32_t ss = min(uint32_t(lane), sp.nsplit - 1);
+        const float2 ml = ld_agent2(a.pml + ((base + ss) * HPK + h) * 2);
+        const float m = in ? ml.x : -INFINITY;
+        const float Mx = wave_max(m);
+        const float f = in ? expf(m - Mx) : 0.0f;
+        const float Ls = group_sum<kWave>(in ? ml.y * f : 0.0f);
+        fw[lane * HPK + h] = f / Ls;  // lane < kMaxSplits = kWave
     }
     __syncthreads();
-    if (tid < HPK) {
-        float Mx = -INFINITY;
-        for (uint32_t ss = 0; ss < sp.nsplit; ++ss) Mx = fmaxf(Mx, mm[ss * HPK + tid]);
-        Mh[tid] = Mx;
-    }
-    __syncthreads();
-    if (uint32_t(tid) < sp.nsplit * HPK) fw[tid] = expf(mm[tid] - Mh[tid % HPK]);
-    __syncthreads();
-    if (tid < HPK) {
-        float Ls = 0.0f;
-        for (uint32_t ss = 0; ss < sp.nsplit; ++ss) Ls = __builtin_fmaf(ll[ss * HPK + tid], fw[ss * HPK + tid], Ls);
-        Mh[tid] = 1.0f / Ls;  // every thread has read Mh before the barrier above
-    }
     if (owner) {
         float r0 = 0.0f, r1 = 0.0f;
         for (uint32_t s0 = 0; s0 < sp.nsplit; s0 += kB) {
@@ -262,12 +257,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
                     r1 = __builtin_fmaf(ov[u].y, f, r1);
                 }
         }
-        ov[0] = make_float2(r0, r1);
-    }
-    __syncthreads();
-    if (owner) {
-        const float li = Mh[hh];
-        reinterpret_cast<float2*>(out + hh * kHeadDim)[dp] = make_float2(ov[0].x * li, ov[0].y * li);
+        reinterpret_cast<float2*>(out + hh * kHeadDim)[dp] = make_float2(r0, r1);
     }
 #undef ARC_ATTN_LOAD
 }
@@ -275,7 +265,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
 template <int HPK>
 constexpr size_t attn_lds_bytes()
 {
-    return (size_t(2 * kStageWords) + HPK * kHeadDim + attn_ew_words<HPK>() + 2 * kMaxSplits * HPK + HPK + 4) * 4;
+    return (size_t(2 * kStageWords) + HPK * kHeadDim + attn_ew_words<HPK>() + 4) * 4;
 }
 
 template <int HPK>
@@ -383,6 +373,9 @@ static int dims_ok(const arc_model_dims& d)
                          d.hidden, d.q_heads, d.kv_heads, d.head_dim, d.ffn, d.vocab, d.layers);
     if (d.hidden / kQK > uint32_t(kPanel) || d.ffn / kQK > uint32_t(kPanel))
         return set_error(ARC_ERR_UNSUPPORTED, "hidden and ffn must be <= %d", kPanel * kQK);
+    // Q6_K tensors are read through 32-bit byte offsets
+    if (uint64_t(d.vocab) * (d.hidden / kQK) * kQ6Bytes > 0xfffffff0ull)
+        return set_error(ARC_ERR_UNSUPPORTED, "output tensor of %u x %u exceeds 4 GiB", d.vocab, d.hidden);
     for (uint32_t l = 0; l < d.layers; ++l)
         if ((d.v_type[l] != kFmtQ4 && d.v_type[l] != kFmtQ6) || (d.down_type[l] != kFmtQ4 && d.down_type[l] != kFmtQ6))
             return set_error(ARC_ERR_UNSUPPORTED, "layer %u: attn_v / ffn_down must be Q4_K or Q6_K", l);

@@ -118,33 +118,45 @@ __device__ __forceinline__ void q4_load(const uint8_t* blk, int v, Q4Blk& o)
     o.qb = ld16_aligned(blk + 80 + v * 16);
 }
 
-// A Q6_K block starts 0 or 2 bytes past a dword boundary.  Each 16-byte
-// chunk is read as a dwordx4 plus the following dword from the dword-aligned
-// block base and kept as read; q6_dot realigns it (by sh bytes) where it is
-// consumed, so nothing waits for a load right after issuing it.  The dwords
-// read cover block bytes [o-2, o+18) for o <= 192: each one holds at least one
-// byte of the block itself, so no read reaches a page the tensor does not
-// touch.  Pieces: 0, 1 ql of both 128-element halves, 2, 3 the matching qh,
-// 4 the int8 scales (its trailing dword holds d).
+// A Q6_K block (210 bytes) starts 0 or 2 bytes past a dword boundary.  It is
+// read with buffer loads over the whole tensor (a uniform descriptor in
+// SGPRs, 32-bit byte offsets: no 64-bit address arithmetic per load).  Each
+// 16-byte chunk is read as a dwordx4 plus the following dword from the
+// dword-aligned address below it and kept as read; q6_dot realigns it (by sh
+// bytes) where it is consumed, so nothing waits for a load right after
+// issuing it.  The dwords read cover block bytes [o-2, o+18) for o <= 192;
+// past the tensor's end the hardware returns zeros instead of reading.
+// Pieces: 0, 1 ql of both 128-element halves, 2, 3 the matching qh, 4 the
+// int8 scales (its trailing dword holds d).
 struct Q6Blk {
     uint32_t w[5][5];
     uint32_t sh;
 };
 
-__device__ __forceinline__ void q6_load(const uint8_t* blk, int v, Q6Blk& o)
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor of `bytes` bytes at `base` (uniform arguments).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tensor_rsrc(const uint8_t* base, uint32_t bytes)
 {
-    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(blk)) & 3u;
-    const uint8_t* b = blk - sh;
-    const uint32_t off[5] = {uint32_t(v) * 16u, 64u + uint32_t(v) * 16u, 128u + uint32_t(v & 1) * 16u,
-                             160u + uint32_t(v & 1) * 16u, 192u};
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, int(bytes), 0x00020000);
+}
+
+// The block at byte offset `off` of a tensor that starts base_sh bytes past
+// the dword-aligned base of descriptor r.
+__device__ __forceinline__ void q6_load(__amdgpu_buffer_rsrc_t r, uint32_t base_sh, uint32_t off, int v, Q6Blk& o)
+{
+    const uint32_t sh = (off + base_sh) & 3u;
+    const uint32_t a = off + base_sh - sh;
+    const uint32_t ql = a + uint32_t(v) * 16u, qh = a + uint32_t(v & 1) * 16u;
+    const uint32_t at[5] = {ql, ql + 64u, qh + 128u, qh + 160u, a + 192u};
 #pragma unroll
     for (int p = 0; p < 5; ++p) {
-        const u32x4a4 x = *reinterpret_cast<const u32x4a4*>(b + off[p]);
+        const u32x4v x = __builtin_amdgcn_raw_buffer_load_b128(r, at[p], 0, 0);
         o.w[p][0] = x.x;
         o.w[p][1] = x.y;
         o.w[p][2] = x.z;
         o.w[p][3] = x.w;
-        o.w[p][4] = *reinterpret_cast<const uint32_t*>(b + off[p] + 16);
+        o.w[p][4] = __builtin_amdgcn_raw_buffer_load_b32(r, at[p] + 16u, 0, 0);
     }
     o.sh = sh;
 }
@@ -436,15 +448,16 @@ __device__ __forceinline__ void blk_dot(const typename BlkOf<FMT>::T (&b)[N], co
         q6_dot<N>(b, xs, v, acc);
 }
 
+// Q4_K and EXEC148 blocks (16- and 4-byte aligned) are read through their
+// address; Q6_K blocks through the tensor's buffer descriptor (q6_load).
 template <int FMT>
 __device__ __forceinline__ void blk_load(const uint8_t* blk, int v, typename BlkOf<FMT>::T& o)
 {
+    static_assert(FMT != kFmtQ6, "Q6_K blocks are read with q6_load");
     if constexpr (FMT == kFmtQ4)
         q4_load(blk, v, o);
-    else if constexpr (FMT == kFmtE148)
-        e148_load(blk, v, o);
     else
-        q6_load(blk, v, o);
+        e148_load(blk, v, o);
 }
 
 // ------------------------------------------------------------- reductions
@@ -780,6 +793,17 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
     const uint32_t S = my_tiles * nj;
 
     auto tile_row = [&](uint32_t tile, int j) { return tile * kTileRows + rg * RPL + j; };
+    // Q6_K: a buffer descriptor over each matrix (the host keeps a Q6_K
+    // tensor below 4 GiB); unused, and removed, for the other formats
+    // (descriptor bases at the dword boundary at or below each tensor; the
+    // last block's final dword holds 2 bytes past the tensor, hence + 4)
+    const uint32_t rows0 = EPI == EPI_QKROPE ? p.row_split : p.rows;
+    const uint8_t* w1 = NMAT == 2 || EPI == EPI_QKROPE ? p.w1 : p.w0;
+    const uint32_t sh0 = uint32_t(reinterpret_cast<uintptr_t>(p.w0)) & 3u;
+    const uint32_t sh1 = uint32_t(reinterpret_cast<uintptr_t>(w1)) & 3u;
+    const __amdgpu_buffer_rsrc_t q6r0 = tensor_rsrc(p.w0 - sh0, uint32_t(uint64_t(rows0) * p.row_bytes) + sh0 + 4u);
+    const __amdgpu_buffer_rsrc_t q6r1 =
+        tensor_rsrc(w1 - sh1, uint32_t(uint64_t(p.rows - (EPI == EPI_QKROPE ? rows0 : 0u)) * p.row_bytes) + sh1 + 4u);
     // Loads are issued unconditionally (indices clamped to valid blocks and
     // rows) so the compiler can count the outstanding loads exactly and wait
     // only for the buffer being consumed, never for the prefetch in flight.
@@ -791,13 +815,27 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
 #pragma unroll
             for (int r = 0; r < RPL; ++r) {
                 const uint32_t row = min(tile_row(tile, r), p.rows - 1);  // clamp: result discarded
-                const uint8_t* base;
-                if constexpr (EPI == EPI_QKROPE)
-                    base = row < p.row_split ? p.w0 + uint64_t(row) * p.row_bytes
-                                             : p.w1 + uint64_t(row - p.row_split) * p.row_bytes;
-                else
-                    base = (m == 0 ? p.w0 : p.w1) + uint64_t(row) * p.row_bytes;
-                blk_load<FMT>(base + uint64_t(kb + bl) * kBB, v, b[m * RPL + r]);
+                if constexpr (FMT == kFmtQ6) {
+                    const uint32_t col = (kb + bl) * uint32_t(kBB);
+                    if constexpr (EPI == EPI_QKROPE) {
+                        if (row < p.row_split)
+                            q6_load(q6r0, sh0, row * uint32_t(p.row_bytes) + col, v, b[m * RPL + r]);
+                        else
+                            q6_load(q6r1, sh1, (row - p.row_split) * uint32_t(p.row_bytes) + col, v,
+                                    b[m * RPL + r]);
+                    } else {
+                        q6_load(m == 0 ? q6r0 : q6r1, m == 0 ? sh0 : sh1, row * uint32_t(p.row_bytes) + col, v,
+                                b[m * RPL + r]);
+                    }
+                } else {
+                    const uint8_t* base;
+                    if constexpr (EPI == EPI_QKROPE)
+                        base = row < p.row_split ? p.w0 + uint64_t(row) * p.row_bytes
+                                                 : p.w1 + uint64_t(row - p.row_split) * p.row_bytes;
+                    else
+                        base = (m == 0 ? p.w0 : p.w1) + uint64_t(row) * p.row_bytes;
+                    blk_load<FMT>(base + uint64_t(kb + bl) * kBB, v, b[m * RPL + r]);
+                }
             }
         }
     };
@@ -1228,6 +1266,8 @@ static int check_shape(int qtype, const void* w, uint32_t rows, uint32_t K)
     const uintptr_t a = reinterpret_cast<uintptr_t>(w);
     if (qtype == kFmtQ4 && (a & 15u)) return set_error(ARC_ERR_INVALID_ARGUMENT, "Q4_K tensor not 16-byte aligned");
     if (qtype == kFmtQ6 && (a & 1u)) return set_error(ARC_ERR_INVALID_ARGUMENT, "Q6_K tensor not 2-byte aligned");
+    if (qtype == kFmtQ6 && uint64_t(rows) * (K / kQK) * kQ6Bytes > 0xfffffff0ull)
+        return set_error(ARC_ERR_UNSUPPORTED, "Q6_K tensor of %u x %u exceeds 4 GiB", rows, K);
     if (qtype == kFmtE148 && (a & 3u)) return set_error(ARC_ERR_INVALID_ARGUMENT, "EXEC148 tensor not 4-byte aligned");
     return ARC_OK;
 }
