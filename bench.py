@@ -279,6 +279,8 @@ def main() -> int:
     ap.add_argument("--no-components", action="store_true", help="skip the config 0 / config 2 legs")
     ap.add_argument("--no-decode", action="store_true", help="skip the 28-layer decode leg")
     ap.add_argument("--decode-steps", type=int, default=64)
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the 256-token prompt pass of the 7B-shaped model (for profiling it alone)")
     ap.add_argument("--decode-eager", action="store_true",
                     help="launch the decode step kernel by kernel instead of replaying its captured graph")
     args = ap.parse_args()
@@ -293,6 +295,14 @@ def main() -> int:
         raise SystemExit("no HIP device visible")
     name, gfx = arc.device_info()
     log(f"device {name} {gfx}")
+
+    if args.prefill_only:
+        d = arc.qwen25_7b_dims()
+        log("prefill: generating the 7B-shaped model")
+        model = arc.Model(d, seed=SEED)
+        print(json.dumps({"prefill": prefill_leg(model, d), "device": f"{name} {gfx}"}))
+        model.close()
+        return 0
 
     B = max(1, args.banks)
     stream = arc.Stream()

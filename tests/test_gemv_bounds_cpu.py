@@ -1,0 +1,89 @@
+"""The bounds model of the packed GEMV (tests/gemv_bounds.py) over the
+launchable layouts and epilogues, over grids from one workgroup to one wave
+tile per wave, and over the Q6_K layouts with four rows per lane that the
+library refuses to launch (one of them, k_gemv<Q6_K, 2, 4, PLAIN, 4>, took a
+GPU memory fault once at 301 x 3584): every weight read, epilogue load, x
+staging access, LDS access and store stays inside its buffer.  A mistake
+planted in the model (an unclamped row or block index) is reported."""
+import itertools
+
+import pytest
+
+import gemv_bounds as gb
+
+SHAPES = [(1, 256), (5, 512), (64, 3584), (301, 3584), (33, 18944)]
+
+
+def grids(c):
+    nb = c.K // 256
+    tr = (64 // (4 * c.bs)) * c.rpl
+    want = max(1, ((c.rows + tr - 1) // tr + c.waves - 1) // c.waves)
+    return sorted({1, want})
+
+
+def run(c, mistake=None):
+    out = []
+    for gx in grids(c):
+        c.gx = gx
+        r = gb.simulate(c, mistake)
+        out.append((gx, r))
+    return out
+
+
+def cases():
+    for fmt in (gb.Q4, gb.Q6, gb.E148):
+        for (bs, rpl), W, (rows, K) in itertools.product(gb.built_layouts(fmt), (4, 8), SHAPES):
+            nb = K // 256
+            yield gb.Config(fmt, bs, rpl, gb.PLAIN, W, rows, K, tensor_align=2 if fmt == gb.Q6 else 0)
+            if fmt == gb.Q4 and rpl <= 2:
+                yield gb.Config(fmt, bs, rpl, gb.SWIGLU, W, rows, K)
+            if nb >= 3:
+                sb = (nb + 2) // 3
+                yield gb.Config(fmt, bs, rpl, gb.PARTIAL, W, rows, K, splits=3, split_bps=sb, nsplit=3,
+                                panel=min(sb, 74))
+            if fmt != gb.E148:
+                yield gb.Config(fmt, bs, rpl, gb.ARGMAX, W, rows, K)
+            if bs >= 8 or rpl == 1:
+                yield gb.Config(fmt, bs, rpl, gb.COLPART, W, rows, K, splits=nb, split_bps=1, nsplit=nb, panel=1)
+
+
+def test_every_launchable_configuration_stays_in_bounds():
+    n = 0
+    for c in cases():
+        for gx, r in run(c):
+            assert not r.violations, (c, gx, r.violations)
+            n += r.checked
+    assert n > 10_000
+
+
+@pytest.mark.parametrize("W", [4, 8])
+@pytest.mark.parametrize("bs", [1, 2])
+@pytest.mark.parametrize("align", [0, 2])
+def test_refused_q6_four_rows_per_lane_layouts_stay_in_bounds(bs, W, align):
+    """The refused layouts' index arithmetic is in bounds too, at the shape
+    that faulted and around it: the fault's cause is not an index of
+    gemv_body (the layout stays refused, its GPU cases skipped)."""
+    for rows in (300, 301, 302, 3584):
+        c = gb.Config(gb.Q6, bs, 4, gb.PLAIN, W, rows, 3584, tensor_align=align)
+        for gx, r in run(c):
+            assert not r.violations, (rows, gx, r.violations)
+
+
+def test_qkrope_and_vstore_epilogues_stay_in_bounds():
+    for fmt in (gb.Q4,):
+        c = gb.Config(fmt, 4, 2, gb.QKROPE, 4, 3584 + 512, 3584, row_split=3584, kv_dim=512, pos=700, max_ctx=701)
+        for gx, r in run(c):
+            assert not r.violations, (gx, r.violations)
+    for fmt in (gb.Q4, gb.Q6):
+        c = gb.Config(fmt, 4, 1, gb.VSTORE, 4, 512, 3584, kv_dim=512, pos=0, max_ctx=1, tensor_align=2)
+        for gx, r in run(c):
+            assert not r.violations, (gx, r.violations)
+
+
+@pytest.mark.parametrize("mistake", ["row", "block"])
+def test_planted_index_mistake_is_reported(mistake):
+    found = False
+    for c in (gb.Config(gb.Q4, 2, 2, gb.PLAIN, 4, 301, 3584), gb.Config(gb.Q6, 4, 1, gb.PLAIN, 4, 5, 512)):
+        for gx, r in run(c, mistake):
+            found |= bool(r.violations)
+    assert found
