@@ -146,6 +146,7 @@ def decode_leg(steps: int, warmup: int, graph: bool = True) -> dict:
                                      "nonfinite": int(nf), "first_tokens": toks[:4].tolist()}
         log(f"decode ctx {ctx}: {steps / dt:.1f} tok/s, {dt / steps * 1e3:.3f} ms/token, {gbs:.0f} GB/s")
     out["kernels_per_step"] = sess.kernels_per_step
+    out["residency"] = sess.residency()  # planned bytes: model arena, KV, working (arc_session_residency)
     sess.close()
     out["prefill"] = prefill_leg(model, d)
     model.close()
