@@ -370,6 +370,152 @@ __device__ __forceinline__ void pf_half(const XSrc& p, PfState<FMT, MB, NF>& s, 
     x_store<MB, 1>(xdst, xr);
 }
 
+// D[m][c]: register i of block mb holds row mb*32 + (i/4)*8 + (lane/32)*4 + i%4
+__device__ __forceinline__ uint32_t acc_row(int mb, int i, int lane)
+{
+    return uint32_t(mb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3));
+}
+
+// ------------------------------------------ gate/up + SwiGLU in 8 waves
+// The fused gate/up GEMM with one weight row per lane (NF = 1): waves 0-3
+// own the tile's 128 gate rows, waves 4-7 its 128 up rows.  A wave then
+// needs half the accumulators of the NF = 2 layout, so two waves fit per
+// SIMD and one wave's dequantisation overlaps the other's MFMAs; every
+// weight is still dequantised once.  Each wave group stages one part of
+// every X tile (threads t & 255 of group g move part g), and SwiGLU is
+// joined through LDS at the end: the gate waves store silu(g) by
+// (row, column), the up waves multiply.
+// Pieces part*MB + sub*NP + i (i < NP, sub*NP + i < MB) of thread t & 255,
+// NP = ceil(MB / 2): each group moves its part in two halves.
+template <int MB>
+constexpr int gu_np()
+{
+    return (MB + 1) / 2;
+}
+
+template <int MB>
+__device__ __forceinline__ void x_fetch_part(const XSrc& xs, uint32_t k0, uint32_t part, int sub,
+                                             u32x4 (&reg)[gu_np<MB>()])
+{
+    constexpr int NP = gu_np<MB>();
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        if (sub * NP + i >= MB) break;
+        const uint32_t soff = (16u * (part * MB + uint32_t(sub * NP + i)) * xs.ldx + k0) * 2u;
+        reg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xs.rsrc, xs.voff, soff, 0));
+    }
+}
+
+template <int MB>
+__device__ __forceinline__ void x_store_part(_Float16* stage, uint32_t part, int sub, const u32x4 (&reg)[gu_np<MB>()])
+{
+    constexpr int NP = gu_np<MB>();
+    const uint32_t t = threadIdx.x & 255u;
+    _Float16* base = stage + (part * MB * 16) * kPfLd + (t >> 4) * kPfLd + (t & 15u) * 8u;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        if (sub * NP + i >= MB) break;
+        *reinterpret_cast<u32x4*>(base + (sub * NP + i) * 16 * kPfLd) = reg[i];
+    }
+}
+
+template <int FMT, int MB, int HB>
+__device__ __forceinline__ void pf_half_gu(const XSrc& p, PfState<FMT, MB, 1>& s, const _Float16* a, uint32_t xk0,
+                                           _Float16* xdst, const uint8_t* const (&wnext)[1], uint32_t kh, uint32_t part,
+                                           half8 (&b0)[1], half8 (&b1)[1])
+{
+    u32x4 xr[gu_np<MB>()];
+    x_fetch_part<MB>(p, xk0, part, 0, xr);
+    if constexpr (HB == 1) load_w<FMT>(wnext[0], kh, s.raw[0]);
+    load_a<MB>(a, s.af);
+    __builtin_amdgcn_sched_barrier(0);
+    pf_step<FMT, MB, 1, HB, 0>(s, a, kh, b0, b1);
+    pf_step<FMT, MB, 1, HB, 1>(s, a, kh, b1, b0);
+    pf_step<FMT, MB, 1, HB, 2>(s, a, kh, b0, b1);
+    pf_step<FMT, MB, 1, HB, 3>(s, a, kh, b1, b0);
+    x_store_part<MB>(xdst, part, 0, xr);
+    x_fetch_part<MB>(p, xk0, part, 1, xr);
+    __builtin_amdgcn_sched_barrier(0);
+    pf_step<FMT, MB, 1, HB, 4>(s, a, kh, b0, b1);
+    pf_step<FMT, MB, 1, HB, 5>(s, a, kh, b1, b0);
+    pf_step<FMT, MB, 1, HB, 6>(s, a, kh, b0, b1);
+    pf_step<FMT, MB, 1, HB, 7>(s, a, kh, b1, b0);
+    x_store_part<MB>(xdst, part, 1, xr);
+}
+
+template <int FMT, int MB>
+__global__ __launch_bounds__(512, 1) void k_pf_gemm_gu(PfGemm p)
+{
+    extern __shared__ __align__(16) _Float16 ash[];  // [2][MB*32][kPfLd]
+    constexpr int kStage = MB * 32 * kPfLd;
+    constexpr int kBB = FMT == kFmtQ4 ? kQ4Bytes : kQ6Bytes;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t part = uint32_t(wave) >> 2, kh = uint32_t(lane) >> 5;
+    const uint32_t c = uint32_t(wave & 3) * 32 + uint32_t(lane & 31);  // column within the tile
+    const uint32_t col = blockIdx.x * 128 + c;
+    const uint8_t* wrow = (part == 0 ? p.w0 : p.w1) + uint64_t(min(col, p.N - 1)) * p.row_bytes;
+
+    PfState<FMT, MB, 1> s;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s.acc[0][mb][i] = 0.0f;
+
+    XSrc xs;
+    xs.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(p.x), (short)0, int(MB * 32 * p.ldx * 2u),
+                                                0x00020000);
+    const uint32_t t = uint32_t(tid) & 255u;
+    xs.voff = ((t >> 4) * p.ldx + (t & 15u) * 8u) * 2u;
+    xs.ldx = p.ldx;
+
+    // prologue: weights of super-block 0, stage 0 = half 0 of super-block 0
+    load_w<FMT>(wrow, kh, s.raw[0]);
+    {
+        u32x4 xr[gu_np<MB>()];
+        x_fetch_part<MB>(xs, 0, part, 0, xr);
+        x_store_part<MB>(ash, part, 0, xr);
+        x_fetch_part<MB>(xs, 0, part, 1, xr);
+        x_store_part<MB>(ash, part, 1, xr);
+    }
+    half8 b0[1], b1[1];
+    decode_w<FMT>(s.raw[0], kh, s.dec[0]);
+    b0[0] = dequant_step<FMT, 0, 0>(s.dec[0]);
+    lds_barrier();
+    const uint32_t ao = (lane & 31) * kPfLd + kh * 16;
+    const _Float16* a0 = ash + ao;
+    const _Float16* a1 = ash + opaque(ao + kStage);
+    for (uint32_t kb = 0; kb < p.nb; ++kb) {
+        const uint32_t kn = kb + 1 < p.nb ? kb + 1 : kb;  // the last super-block re-loads and re-stages itself
+        const uint8_t* wn[1] = {wrow + uint64_t(kn) * kBB};
+        pf_half_gu<FMT, MB, 0>(xs, s, a0, kb * kQK + kPfKT, ash + kStage, wn, kh, part, b0, b1);
+        lds_barrier();
+        pf_half_gu<FMT, MB, 1>(xs, s, a1, kn * kQK, ash, wn, kh, part, b0, b1);
+        lds_barrier();
+    }
+
+    // SwiGLU across the wave groups: silu(gate) by (row, column) in the free stages
+    float* sg = reinterpret_cast<float*>(ash);  // [MB*32][128]
+    if (part == 0) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float g = s.acc[0][mb][i];
+                sg[acc_row(mb, i, lane) * 128 + c] = g / (1.0f + expf(-g));
+            }
+    }
+    __syncthreads();
+    if (part == 1 && col < p.N) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t m = acc_row(mb, i, lane);
+                if (m < p.M) p.s[uint64_t(m) * p.lds_out + col] = _Float16(sg[m * 128 + c] * s.acc[0][mb][i]);
+            }
+    }
+}
+
 // Y = X W^T over super-blocks [kb0, kb1) of K for MB*32 rows of X.
 // Workgroup: 4 waves, one per SIMD; lane (l%32) of wave w owns weight row(s)
 //   SWIGLU (NF = 2): gate and up row c = tile*128 + w*32 + l%32, and
@@ -810,6 +956,31 @@ hipError_t launch_gemm_t(const PfGemm& p, uint32_t gx, uint32_t splits, hipStrea
     return hipGetLastError();
 }
 
+template <int MB>
+hipError_t launch_gu_t(const PfGemm& p, uint32_t gx, hipStream_t st)
+{
+    const size_t lds = size_t(2) * MB * 32 * kPfLd * sizeof(_Float16);
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm_gu<kFmtQ4, MB>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_pf_gemm_gu<kFmtQ4, MB>), dim3(gx), dim3(512), lds, st, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_gateup(const PfGemm& p, uint32_t mb, uint32_t gx, hipStream_t st)
+{
+    switch (mb) {
+    case 1: return launch_gu_t<1>(p, gx, st);
+    case 2: return launch_gu_t<2>(p, gx, st);
+    case 4: return launch_gu_t<4>(p, gx, st);
+    default: return launch_gu_t<8>(p, gx, st);
+    }
+}
+
 template <int FMT, int NF, bool SW>
 hipError_t launch_gemm_mb(const PfGemm& p, uint32_t mb, uint32_t gx, uint32_t splits, hipStream_t st)
 {
@@ -1012,7 +1183,7 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             u.bps = g.nb;
             u.s = pf->xs;
             u.lds_out = F;
-            if ((rc = chk(launch_gemm_mb<kFmtQ4, 2, true>(u, mb, (F + 127) / 128, 1, st), "gate/up"))) return rc;
+            if ((rc = chk(launch_gateup(u, mb, (F + 127) / 128, st), "gate/up"))) return rc;
             // down + residual (+ the next layer's attention norm)
             PfGemm dn = g;
             dn.x = pf->xs;
