@@ -58,232 +58,288 @@ __device__ __host__ inline AttnSplit attn_split(uint32_t T)
     return AttnSplit{nch, cps, (nch + cps - 1) / cps};
 }
 
-// LDS of k_attn (32-bit words): per stage K transposed as half2 pairs of
-// dims [64 dim pairs][kChunk + 1 pad] and V as [kChunk][64 dim pairs].
-constexpr int kKtStride = kChunk + 1;
-constexpr int kStageWords = (kHeadDim / 2) * kKtStride + kChunk * (kHeadDim / 2);
-constexpr int kAttnThreads = 512;  // 8 waves: wave w computes query head w of the group
+// k_attn: 4 waves per workgroup; wave w takes positions 16w .. 16w+15 of
+// every chunk of kChunk positions, with its own running softmax state.
+constexpr int kAttnWaves = 4;
+constexpr int kAttnThreads = kAttnWaves * kWave;
+constexpr int kAttnTile = 16;  // positions per wave and chunk (the MFMA rows)
+static_assert(kChunk == kAttnWaves * kAttnTile, "one 16-position MFMA tile per wave");
+static_assert(kHeadDim == 2 * kWave, "V sum: one dim pair per lane");
 static_assert(kMaxSplits <= kWave, "the merge takes one split per lane");
 constexpr int kAttnMergeBatch = 16;  // split outputs loaded per batch in the merge
 constexpr uint32_t kAttnEarlySplits = 8;  // splits that load before reading the position
-// The scores' softmax weights (one kChunk row per head wave), reused by the
-// merge for the split weights ([kMaxSplits][HPK]).
-template <int HPK>
-constexpr int attn_ew_words()
-{
-    constexpr int rows = HPK * kChunk, merge = kMaxSplits * HPK;
-    return rows > merge ? rows : merge;
-}
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // Cached GQA of one new position (flash decoding in one launch).  Workgroup
-// (s, g) covers the chunks of split s for kv head g; wave h computes query
-// head h of the group (lane = position for the scores, lane = dim pair for
-// the weighted V sum), so no reduction crosses waves.  Each chunk's K and V
-// are read once, coalesced, by all 512 threads and staged in LDS (K
-// transposed), double-buffered: the next chunk's loads are in flight while
-// one is used (splits 0..7 issue their first chunk's before the position is
-// read: its rows are clamped to the cache and masked later).  Per chunk and head:
-// scores, chunk softmax, weighted V sum, folded into the wave's running
-// (max, sum, o).  A single split writes the output; otherwise each split's
-// (m, l, o) goes to memory past the L2 (st_agent) and the last workgroup of
-// kv head g to arrive merges the splits in split order: M = max m_s,
-// f_s = e^(m_s - M), L = sum l_s f_s, out = sum o_s (f_s / L).  Every
-// reduction has a fixed order, so the result does not depend on which
+// (s, g) covers the chunks of split s for kv head g and all HPK query heads
+// of that kv head.  Wave w owns positions 16w .. 16w+15 of each chunk and
+// keeps its own running (max, sum, o) per head, so the chunk loop has no
+// barrier:
+//  scores  S^T = K Q^T on v_mfma_f32_16x16x32_f16.  A = K rows straight from
+//          the cache (lane -> position lane%16; K slot (lane/16, j) of step
+//          ks = dim 32*(lane/16) + 8*ks + j, so a lane's operand is 64
+//          contiguous bytes of its row), B = Q^T (lane -> query head
+//          lane%16, zero past HPK) split into fp16 hi + lo parts (q = hi + lo
+//          to 2^-22 relative; the K*hi and K*lo products are exact in the
+//          fp32 accumulator).  D: lane -> head lane%16, positions
+//          4*(lane/16) + i.
+//  softmax tile maximum per head (row exchanges), weights e^(x - max) to
+//          the wave's LDS rows [position][head], read back by the same wave
+//          (LDS operations of a wave complete in order).
+//  V sum   lane -> dim pair (2 lane, 2 lane + 1), V read as fp16 straight
+//          from the cache, one 256-byte row per load; o[head] += e * v on
+//          v_fma_mix (fp32 weights, exact products).
+// The next chunk's K and V loads are in flight while one is used (splits
+// 0..7 issue their first chunk's before the position is read: rows clamped
+// to the cache, masked later).  At the split's end the 4 waves' states are
+// combined through LDS in wave order.  A single split writes the output;
+// otherwise each split's (m, l, o) goes to memory past the L2 (st_agent) and
+// the last workgroup of kv head g to arrive merges the splits in split order:
+// M = max m_s, f_s = e^(m_s - M), L = sum l_s f_s, out = sum o_s (f_s / L).
+// Every reduction has a fixed order, so the result does not depend on which
 // workgroup arrives last.
 // Semantics: src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1177-1212,
 // shaders/p7_attention_kv_online.comp (kv head = q head / (q_heads/kv_heads)).
 template <int HPK>
 __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
 {
-    extern __shared__ __align__(16) uint32_t smw[];
-    auto stage = [&](uint32_t i) { return smw + (i & 1u) * kStageWords; };
-    float* qs = reinterpret_cast<float*>(smw + 2 * kStageWords);  // [HPK][128]
-    float* ew = qs + HPK * kHeadDim;                               // [HPK waves][kChunk]; merge: [kMaxSplits][HPK]
-    uint32_t* flag = reinterpret_cast<uint32_t*>(ew + attn_ew_words<HPK>());
+    __shared__ __align__(16) float pw[kAttnWaves][kAttnTile][8];  // per wave: weights [position][head]
+    __shared__ __align__(16) float fow[kAttnWaves][8];            // per wave: rescale per head
+    __shared__ float mw[kAttnWaves][8], lw[kAttnWaves][8];         // split end: wave (max, sum) per head
+    __shared__ __align__(16) float ow[kAttnWaves][HPK][kHeadDim];  // split end: wave o per head
+    __shared__ float fw[kMaxSplits][HPK];                          // merge: split weights
+    __shared__ uint32_t flag;
 
     const uint32_t s = blockIdx.x, g = blockIdx.y;
-    const uint32_t kvd = a.kv_heads * kHeadDim;
+    const uint64_t kvd = uint64_t(a.kv_heads) * kHeadDim;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int r16 = lane & 15, grp = lane >> 4;  // scores: MFMA row/column, K-slot group
 
-    // cooperative chunk load: 16 lanes per row, 16 B each (dims 8o .. 8o+7);
-    // thread t covers rows t/16 and t/16 + 32 of K and of V
-    const uint32_t lrow = uint32_t(tid) >> 4, oct = tid & 15;
-    const _Float16* kbase = a.kc + g * kHeadDim + 8 * oct;
-    const _Float16* vbase = a.vc + g * kHeadDim + 8 * oct;
-    uint4 rk0, rk1, rv0, rv1;
-#define ARC_ATTN_LOAD(t0, tmax)                                                                        \
-    do {                                                                                               \
-        const uint64_t r0 = min((t0) + lrow, (tmax)), r1 = min((t0) + lrow + 32u, (tmax));             \
-        rk0 = *reinterpret_cast<const uint4*>(kbase + r0 * kvd);                                       \
-        rv0 = *reinterpret_cast<const uint4*>(vbase + r0 * kvd);                                       \
-        rk1 = *reinterpret_cast<const uint4*>(kbase + r1 * kvd);                                       \
-        rv1 = *reinterpret_cast<const uint4*>(vbase + r1 * kvd);                                       \
-    } while (0)
-    // K words go to their dim-pair rows (transposed), V rows as read
-    auto put = [](uint32_t* st, uint32_t p, uint32_t o, const uint4& k, const uint4& v) {
-        st[(4 * o + 0) * kKtStride + p] = k.x;
-        st[(4 * o + 1) * kKtStride + p] = k.y;
-        st[(4 * o + 2) * kKtStride + p] = k.z;
-        st[(4 * o + 3) * kKtStride + p] = k.w;
-        *reinterpret_cast<uint4*>(st + (kHeadDim / 2) * kKtStride + p * (kHeadDim / 2) + 4 * o) = v;
+    const _Float16* kb = a.kc + g * kHeadDim + 32 * grp;
+    const _Float16* vb = a.vc + g * kHeadDim + 2 * lane;
+    uint4 kr[4];            // K row t0 + 16w + r16, dims 32grp .. 32grp+31
+    uint32_t vr[kAttnTile];  // V rows t0 + 16w + j, dims 2 lane, 2 lane + 1
+    auto load = [&](uint32_t t0, uint32_t tmax) {
+        const uint32_t tw = t0 + kAttnTile * w;
+        const uint4* kp = reinterpret_cast<const uint4*>(kb + uint64_t(min(tw + r16, tmax)) * kvd);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[i] = kp[i];
+#pragma unroll
+        for (int j = 0; j < kAttnTile; ++j)
+            vr[j] = *reinterpret_cast<const uint32_t*>(vb + uint64_t(min(tw + j, tmax)) * kvd);
     };
 
     // Splits 0..7 take part in every plan above 448 positions: they issue
-    // their first chunk's loads before the position is known (rows clamped
-    // to the cache, masked later).  The others read the position first, so
-    // the splits a short context leaves idle read nothing (at 512 positions
-    // 224 of 256 workgroups; measured 575 vs 568 tok/s, 522 vs 517 at 4096).
+    // their first chunk's loads before the position is known.  The others
+    // read the position first, so the splits a short context leaves idle
+    // read nothing.
     const bool early = s < kAttnEarlySplits;
-    if (early) ARC_ATTN_LOAD(s * kChunk, a.max_ctx - 1);  // chunk s: the first chunk of split s when cps = 1
-    for (uint32_t i = tid; i < HPK * kHeadDim; i += kAttnThreads) qs[i] = a.q[g * HPK * kHeadDim + i];
-
+    if (early) load(s * kChunk, a.max_ctx - 1);  // chunk s: the first chunk of split s when cps = 1
+    float4 qv[8];
+    {
+        const float4* qp = reinterpret_cast<const float4*>(a.q + (uint64_t(g) * HPK + min(r16, HPK - 1)) * kHeadDim + 32 * grp);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qv[i] = qp[i];
+    }
     const uint32_t T = a.ctl->pos + 1;
     const AttnSplit sp = attn_split(T);
     if (s >= sp.nsplit) return;  // whole workgroup: not part of this position's plan
     const uint32_t c0 = s * sp.cps, c1 = min(c0 + sp.cps, sp.nch);
-    if (sp.cps != 1 || !early) ARC_ATTN_LOAD(c0 * kChunk, T - 1);
-    put(stage(0), lrow, oct, rk0, rv0);
-    put(stage(0), lrow + 32u, oct, rk1, rv1);
+    if (sp.cps != 1 || !early) load(c0 * kChunk, T - 1);
+
+    half8_t qh[4], ql[4];  // B operand: head r16 (zero past HPK), dims 32grp + 8ks .. +7
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const float f[8] = {qv[2 * ks].x, qv[2 * ks].y, qv[2 * ks].z, qv[2 * ks].w,
+                            qv[2 * ks + 1].x, qv[2 * ks + 1].y, qv[2 * ks + 1].z, qv[2 * ks + 1].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float x = r16 < HPK ? f[j] : 0.0f;
+            const _Float16 hi = static_cast<_Float16>(x);
+            qh[ks][j] = hi;
+            ql[ks][j] = static_cast<_Float16>(x - static_cast<float>(hi));
+        }
+    }
+
+    float o0[HPK], o1[HPK];  // this wave's V sums: head h, dims 2 lane, 2 lane + 1
+#pragma unroll
+    for (int h = 0; h < HPK; ++h) o0[h] = o1[h] = 0.0f;
+    float M = -INFINITY, Ls = 0.0f;  // head r16: running max, this lane's share of the running sum
+    float (*pwr)[8] = pw[w];
+    for (uint32_t c = c0; c < c1; ++c) {
+        const uint32_t tw = c * kChunk + kAttnTile * w;
+        uint4 kc[4];
+        uint32_t vc[kAttnTile];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kc[i] = kr[i];
+#pragma unroll
+        for (int j = 0; j < kAttnTile; ++j) vc[j] = vr[j];
+        if (c + 1 < c1) load((c + 1) * kChunk, T - 1);
+
+        f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const half8_t kf = __builtin_bit_cast(half8_t, kc[ks]);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[ks], d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[ks], d, 0, 0, 0);
+        }
+        float x[4], m = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[i] = tw + 4u * grp + i < T ? d[i] * a.scale : -INFINITY;
+            m = fmaxf(m, x[i]);
+        }
+        m = xor_max<16>(m);
+        m = xor_max<32>(m);
+        const float Mn = fmaxf(M, m);
+        const float Mr = Mn == -INFINITY ? 0.0f : Mn;  // a wave may not have seen a position < T yet
+        const float fo = expf(M - Mr);                 // M = -inf: 0
+        float es = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float e = expf(x[i] - Mr);  // masked: e^-inf = 0
+            es += e;
+            if (r16 < HPK) pwr[4 * grp + i][r16] = e;
+        }
+        Ls = Ls * fo + es;
+        M = Mn;
+        if (grp == 0 && r16 < HPK) fow[w][r16] = fo;
+
+        const float4 f0 = *reinterpret_cast<const float4*>(fow[w]), f1 = *reinterpret_cast<const float4*>(fow[w] + 4);
+        const float fh[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+#pragma unroll
+        for (int h = 0; h < HPK; ++h) {
+            o0[h] *= fh[h];
+            o1[h] *= fh[h];
+        }
+#pragma unroll
+        for (int j = 0; j < kAttnTile; ++j) {
+            const float4 p0 = *reinterpret_cast<const float4*>(pwr[j]);
+            const float4 p1 = *reinterpret_cast<const float4*>(pwr[j] + 4);
+            const float ph[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+            for (int h = 0; h < HPK; ++h) {
+                o0[h] = fmix(vc[j], false, ph[h], o0[h]);
+                o1[h] = fmix(vc[j], true, ph[h], o1[h]);
+            }
+        }
+    }
+
+    // the waves' states into LDS, combined per (head, dim quad) in wave order
+    Ls = xor_sum<16>(Ls);
+    Ls = xor_sum<32>(Ls);
+    if (grp == 0 && r16 < HPK) {
+        mw[w][r16] = M;
+        lw[w][r16] = Ls;
+    }
+#pragma unroll
+    for (int h = 0; h < HPK; ++h) reinterpret_cast<float2*>(ow[w][h])[lane] = make_float2(o0[h], o1[h]);
     __syncthreads();
 
-    const int h = w;  // this wave's head (waves h >= HPK only load)
-    float o0 = 0.0f, o1 = 0.0f, M = -INFINITY, L = 0.0f;
-    for (uint32_t c = c0; c < c1; ++c) {
-        const uint32_t* st = stage(c - c0);
-        if (c + 1 < c1) ARC_ATTN_LOAD((c + 1) * kChunk, T - 1);
-        const uint32_t t0 = c * kChunk, nt = min(uint32_t(kChunk), T - t0);
-        if (h < HPK) {
-            // scores: lane = position, K consumed as fp16 (v_fma_mix)
-            const float* qh = qs + h * kHeadDim;
-            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four independent chains
-#pragma unroll 8
-            for (int dp = 0; dp < kHeadDim / 2; dp += 2) {
-                const float4 q4 = *reinterpret_cast<const float4*>(qh + 2 * dp);
-                const uint32_t k0 = st[dp * kKtStride + lane], k1 = st[(dp + 1) * kKtStride + lane];
-                acc[0] = fmix(k0, false, q4.x, acc[0]);
-                acc[1] = fmix(k0, true, q4.y, acc[1]);
-                acc[2] = fmix(k1, false, q4.z, acc[2]);
-                acc[3] = fmix(k1, true, q4.w, acc[3]);
-            }
-            const float sdot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-            const bool valid = uint32_t(lane) < nt;
-            const float x = valid ? sdot * a.scale : -INFINITY;
-            const float m = wave_max(x);
-            const float e = valid ? expf(x - m) : 0.0f;
-            const float l = group_sum<kWave>(e);
-            ew[h * kChunk + lane] = e;  // read back by this wave only (in-order LDS)
-            // weighted V: lane = dim pair (2 lane, 2 lane + 1)
-            const uint32_t* vs = st + (kHeadDim / 2) * kKtStride;
-            float a0[2] = {0.0f, 0.0f}, a1[2] = {0.0f, 0.0f};  // even / odd positions
-#pragma unroll 4
-            for (int p = 0; p < kChunk; p += 4) {
-                const float4 e4 = *reinterpret_cast<const float4*>(ew + h * kChunk + p);
-                const float ee[4] = {e4.x, e4.y, e4.z, e4.w};
+    const bool owner = tid < HPK * (kHeadDim / 4);  // thread -> head hh, dims 4 dq4 .. +3
+    const uint32_t hh = min(uint32_t(tid) / (kHeadDim / 4), uint32_t(HPK - 1)), dq4 = uint32_t(tid) % (kHeadDim / 4);
+    float Msp = -INFINITY, Lsp = 0.0f;
+    float4 osp = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    {
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const uint32_t v2 = vs[(p + u) * (kHeadDim / 2) + lane];
-                    a0[u & 1] = fmix(v2, false, ee[u], a0[u & 1]);
-                    a1[u & 1] = fmix(v2, true, ee[u], a1[u & 1]);
-                }
-            }
-            const float Mn = fmaxf(M, m);
-            const float fo = expf(M - Mn), fc = expf(m - Mn);  // M = -inf first: fo = 0
-            o0 = o0 * fo + (a0[0] + a0[1]) * fc;
-            o1 = o1 * fo + (a1[0] + a1[1]) * fc;
-            L = L * fo + l * fc;
-            M = Mn;
+        for (int v = 0; v < kAttnWaves; ++v) Msp = fmaxf(Msp, mw[v][hh]);  // finite: the split holds a position < T
+#pragma unroll
+        for (int v = 0; v < kAttnWaves; ++v) {
+            const float f = expf(mw[v][hh] - Msp);  // a wave without positions < T: e^-inf = 0
+            const float4 ov = reinterpret_cast<const float4*>(ow[v][hh])[dq4];
+            Lsp = __builtin_fmaf(lw[v][hh], f, Lsp);
+            osp.x = __builtin_fmaf(ov.x, f, osp.x);
+            osp.y = __builtin_fmaf(ov.y, f, osp.y);
+            osp.z = __builtin_fmaf(ov.z, f, osp.z);
+            osp.w = __builtin_fmaf(ov.w, f, osp.w);
         }
-        if (c + 1 < c1) {
-            put(stage(c + 1 - c0), lrow, oct, rk0, rv0);
-            put(stage(c + 1 - c0), lrow + 32u, oct, rk1, rv1);
-        }
-        __syncthreads();
     }
 
     float* out = a.out + uint64_t(g) * HPK * kHeadDim;
     const uint64_t base = uint64_t(g) * kMaxSplits;
     if (sp.nsplit == 1) {
-        if (h < HPK) {
-            const float li = 1.0f / L;
-            reinterpret_cast<float2*>(out + h * kHeadDim)[lane] = make_float2(o0 * li, o1 * li);
+        if (owner) {
+            const float li = 1.0f / Lsp;
+            reinterpret_cast<float4*>(out + hh * kHeadDim)[dq4] = make_float4(osp.x * li, osp.y * li, osp.z * li, osp.w * li);
         }
         return;
     }
     // this split's partials, written past the L2 for the merging workgroup
-    if (h < HPK) {
-        float* po = a.po + ((base + s) * HPK + h) * kHeadDim + 2 * lane;
-        st_agent(po, o0);
-        st_agent(po + 1, o1);
-        if (lane == 0) {
-            st_agent(a.pml + ((base + s) * HPK + h) * 2, M);
-            st_agent(a.pml + ((base + s) * HPK + h) * 2 + 1, L);
+    if (owner) {
+        float* po = a.po + ((base + s) * HPK + hh) * kHeadDim + 4 * dq4;
+        st_agent(po, osp.x);
+        st_agent(po + 1, osp.y);
+        st_agent(po + 2, osp.z);
+        st_agent(po + 3, osp.w);
+        if (dq4 == 0) {
+            st_agent(a.pml + ((base + s) * HPK + hh) * 2, Msp);
+            st_agent(a.pml + ((base + s) * HPK + hh) * 2 + 1, Lsp);
         }
     }
-    if (!arrive_last(a.counter + g, sp.nsplit, flag)) return;
+    if (!arrive_last(a.counter + g, sp.nsplit, &flag)) return;
 
-    // merge (last workgroup of kv head g).  Wave h, lane = split: the split
-    // weights w_s = e^(m_s - M) / L of head h (M and L by wave reductions)
-    // into LDS; then thread -> (head hh, dims 2dp, 2dp+1) sums the splits' o
-    // weighted, in split order, loads in batches of kB (the first batch is
-    // issued before the weights are known).
-    float* fw = ew;  // [kMaxSplits][HPK] split weights (ew is free now)
-    const bool owner = uint32_t(tid) < HPK * (kHeadDim / 2);
-    const uint32_t hh = uint32_t(tid) / (kHeadDim / 2), dp = uint32_t(tid) % (kHeadDim / 2);
-    const float* src = a.po + (base * HPK + min(hh, uint32_t(HPK - 1))) * kHeadDim + 2 * dp;
-    constexpr int kB = kAttnMergeBatch;
-    float2 ov[kB];
-    if (owner)
+    // merge (last workgroup of kv head g).  Wave w, lane = split: the split
+    // weights w_s = e^(m_s - M) / L of heads w, w + 4 (M and L by wave
+    // reductions) into LDS; then thread -> (head hh, dims 4dq4 .. +3) sums
+    // the splits' o weighted, in split order, loads in batches of kB (the
+    // first batch is issued right after the (m, l) loads).
+    const bool in = uint32_t(lane) < sp.nsplit;
+    const uint32_t ss = min(uint32_t(lane), sp.nsplit - 1);
+    float2 ml[2];
 #pragma unroll
-        for (int u = 0; u < kB; ++u) ov[u] = ld_agent2(src + uint64_t(min(uint32_t(u), sp.nsplit - 1)) * HPK * kHeadDim);
-    if (h < HPK) {
-        const bool in = uint32_t(lane) < sp.nsplit;
-        const uint32_t ss = min(uint32_t(lane), sp.nsplit - 1);
-        const float2 ml = ld_agent2(a.pml + ((base + ss) * HPK + h) * 2);
-        const float m = in ? ml.x : -INFINITY;
-        const float Mx = wave_max(m);
-        const float f = in ? expf(m - Mx) : 0.0f;
-        const float Ls = group_sum<kWave>(in ? ml.y * f : 0.0f);
-        fw[lane * HPK + h] = f / Ls;  // lane < kMaxSplits = kWave
+    for (int k = 0; k < 2; ++k) {
+        const uint32_t h = min(uint32_t(w + kAttnWaves * k), uint32_t(HPK - 1));
+        ml[k] = ld_agent2(a.pml + ((base + ss) * HPK + h) * 2);
+    }
+    const float* src = a.po + (base * HPK + hh) * kHeadDim + 4 * dq4;
+    constexpr int kB = kAttnMergeBatch;
+    float4 ov[kB];
+    auto fetch = [&](uint32_t s0) {
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+            const float* p = src + uint64_t(min(s0 + u, sp.nsplit - 1)) * HPK * kHeadDim;
+            const float2 lo = ld_agent2(p), hi = ld_agent2(p + 2);
+            ov[u] = make_float4(lo.x, lo.y, hi.x, hi.y);
+        }
+    };
+    if (owner) fetch(0);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int h = w + kAttnWaves * k;
+        if (h < HPK) {
+            const float m = in ? ml[k].x : -INFINITY;
+            const float Mx = wave_max(m);
+            const float f = in ? expf(m - Mx) : 0.0f;
+            const float Lsum = group_sum<kWave>(in ? ml[k].y * f : 0.0f);
+            fw[lane][h] = f / Lsum;  // lane < kMaxSplits = kWave
+        }
     }
     __syncthreads();
     if (owner) {
-        float r0 = 0.0f, r1 = 0.0f;
+        float4 r = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         for (uint32_t s0 = 0; s0 < sp.nsplit; s0 += kB) {
-            if (s0 != 0)
-#pragma unroll
-                for (int u = 0; u < kB; ++u)
-                    ov[u] = ld_agent2(src + uint64_t(min(s0 + u, sp.nsplit - 1)) * HPK * kHeadDim);
+            if (s0 != 0) fetch(s0);
 #pragma unroll
             for (int u = 0; u < kB; ++u)
                 if (s0 + u < sp.nsplit) {
-                    const float f = fw[(s0 + u) * HPK + hh];
-                    r0 = __builtin_fmaf(ov[u].x, f, r0);
-                    r1 = __builtin_fmaf(ov[u].y, f, r1);
+                    const float f = fw[s0 + u][hh];
+                    r.x = __builtin_fmaf(ov[u].x, f, r.x);
+                    r.y = __builtin_fmaf(ov[u].y, f, r.y);
+                    r.z = __builtin_fmaf(ov[u].z, f, r.z);
+                    r.w = __builtin_fmaf(ov[u].w, f, r.w);
                 }
         }
-        reinterpret_cast<float2*>(out + hh * kHeadDim)[dp] = make_float2(r0, r1);
+        reinterpret_cast<float4*>(out + hh * kHeadDim)[dq4] = r;
     }
-#undef ARC_ATTN_LOAD
-}
-
-template <int HPK>
-constexpr size_t attn_lds_bytes()
-{
-    return (size_t(2 * kStageWords) + HPK * kHeadDim + attn_ew_words<HPK>() + 4) * 4;
 }
 
 template <int HPK>
 static void launch_attn_hpk(const AttnParams& ap, dim3 grid, hipStream_t st)
 {
-    constexpr size_t lds = attn_lds_bytes<HPK>();
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn<HPK>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  int(lds));
-        attr = true;
-    }
     if (g_dry_run) return;
-    hipLaunchKernelGGL(k_attn<HPK>, grid, dim3(kAttnThreads), lds, st, ap);
+    hipLaunchKernelGGL(k_attn<HPK>, grid, dim3(kAttnThreads), 0, st, ap);
 }
 
 // hpk is 1..kMaxHpk (checked with the model dims)
@@ -301,9 +357,9 @@ static void launch_attn(const AttnParams& ap, dim3 grid, hipStream_t st)
     }
 }
 static_assert(kMaxHpk == 8, "launch_attn instantiates 1..8");
-static_assert(kMaxHpk <= kAttnThreads / kWave, "one wave per query head of a kv head");
-static_assert(kMaxHpk * (kHeadDim / 2) <= kAttnThreads && kMaxSplits * kMaxHpk <= kAttnThreads,
-              "merge: one thread per (head, dim pair) and per (split, head)");
+static_assert(kMaxHpk <= 16, "query heads of a kv head fit the 16 MFMA columns");
+static_assert(kMaxHpk * (kHeadDim / 4) <= kAttnThreads && kMaxHpk <= 2 * kAttnWaves,
+              "merge: one thread per (head, dim quad); two heads per wave for the split weights");
 
 }  // namespace arc
 

@@ -124,6 +124,50 @@ __device__ __forceinline__ float dpp_f(float v)
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
 }
 
+// Row exchanges of gfx950 between two registers: v_permlane16_swap swaps
+// the odd 16-lane rows of `a` with the even rows of `b`; v_permlane32_swap
+// swaps the upper 32 lanes of `a` with the lower 32 of `b`.  Afterwards lane
+// l holds a[l] and a[l ^ 16] (resp. ^ 32) where that bit of l is clear, and
+// b[l ^ 16] and b[l] where it is set, so a + b is the pairwise sum of `a` in
+// the first half of the lanes and of `b` in the other.  Inline asm: the
+// compiler's builtins for these return the first result as both results.
+// The s_nop pads cover the VALU-write -> permlane-read and permlane-write ->
+// VALU-read hazards.
+__device__ __forceinline__ void permlane16_swap(uint32_t& a, uint32_t& b)
+{
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane32_swap(uint32_t& a, uint32_t& b)
+{
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+// v[l] and v[l ^ 16] (XOR=16) or v[l] and v[l ^ 32] (XOR=32), in an order
+// that depends on the lane; callers combine them commutatively.
+template <int XOR>
+__device__ __forceinline__ void xor_pair(float v, float& x, float& y)
+{
+    static_assert(XOR == 16 || XOR == 32, "row exchanges only");
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    if constexpr (XOR == 16) permlane16_swap(a, b);
+    else permlane32_swap(a, b);
+    x = __builtin_bit_cast(float, a);
+    y = __builtin_bit_cast(float, b);
+}
+template <int XOR>
+__device__ __forceinline__ float xor_sum(float v)
+{
+    float x, y;
+    xor_pair<XOR>(v, x, y);
+    return x + y;
+}
+template <int XOR>
+__device__ __forceinline__ float xor_max(float v)
+{
+    float x, y;
+    xor_pair<XOR>(v, x, y);
+    return fmaxf(x, y);
+}
+
 // Sum over aligned groups of N consecutive lanes (N a power of two <= 64);
 // every lane of the group receives the group total.  The combination order
 // is fixed, so results are deterministic.
@@ -134,8 +178,8 @@ __device__ __forceinline__ float group_sum(float v)
     if constexpr (N >= 4) v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]: lane ^ 2
     if constexpr (N >= 8) v += dpp_f<0x141>(v);   // row_half_mirror: other quad of 8
     if constexpr (N >= 16) v += dpp_f<0x140>(v);  // row_mirror: other 8 of 16
-    if constexpr (N >= 32) v += __shfl_xor(v, 16);
-    if constexpr (N >= 64) v += __shfl_xor(v, 32);
+    if constexpr (N >= 32) v = xor_sum<16>(v);
+    if constexpr (N >= 64) v = xor_sum<32>(v);
     return v;
 }
 
@@ -157,9 +201,12 @@ __device__ inline float block_sum(float v, float* red)
 
 __device__ __forceinline__ float wave_max(float v)
 {
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    v = xor_max<16>(v);
+    return xor_max<32>(v);
 }
 
 // ----------------------------------------------- cross-workgroup hand-off
