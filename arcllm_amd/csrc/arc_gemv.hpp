@@ -521,20 +521,61 @@ __device__ __forceinline__ void scale_group(float4 (&q)[4], float inv, const flo
     }
 }
 
+// The first groups of x a thread stages (with the fused RMSNorm: its one
+// first group, and that group of the norm weights), loaded before the
+// weight ring's first loads.  Loads complete in issue order, so staging
+// then waits for x alone, not for the ring's HBM loads behind it.  With
+// 8-wave workgroups these are all of the thread's groups of an 80-block
+// panel (the FFN down's 74 blocks: 1184 groups over 512 threads, 3 each),
+// so a wide panel waits for one round trip, not one per group; 4-wave
+// workgroups stage at most 37 blocks (wider panels take 8 waves) and spend
+// their registers on the prefetch ring.
+template <int NT>
+struct XPre {
+    static constexpr int G = NT >= 512 ? (kPanel * 16 + NT - 1) / NT : 1;
+    float4 q[G][4];
+    float4 w[4];
+};
+
 template <int FMT, int NT>
-__device__ void stage_x(float* lds, const float* __restrict__ x, uint32_t b0, uint32_t nbl, bool norm,
+__device__ __forceinline__ void x_pre(XPre<NT>& pre, const float* __restrict__ x, uint32_t b0, uint32_t nbl, bool rms,
+                                      const float* __restrict__ normw)
+{
+    // Indices are clamped into the panel instead of branching around the
+    // loads (registers loaded under a branch are waited for where it joins);
+    // groups past the panel load a valid group and are not stored.  The
+    // fused RMSNorm stages the whole row (b0 = 0), so its first group is
+    // q[0] here too; the embedding row (erow) is decoded in stage_x_rms.
+    const uint32_t last = nbl * 16u - 1u;
+#pragma unroll
+    for (int i = 0; i < XPre<NT>::G; ++i)
+        ld_group(x + group_elem<FMT>(b0, min(threadIdx.x + uint32_t(i * NT), last)), pre.q[i]);
+    if (rms) ld_group(normw + group_elem<FMT>(0, min(uint32_t(threadIdx.x), last)), pre.w);
+}
+
+template <int FMT, int NT>
+__device__ void stage_x(float* lds, XPre<NT>& pre, const float* __restrict__ x, uint32_t b0, uint32_t nbl, bool norm,
                         float inv, const float* __restrict__ normw)
 {
-    for (uint32_t gi = threadIdx.x; gi < nbl * 16u; gi += NT) {
-        const uint32_t e = group_elem<FMT>(b0, gi);
-        float4 q[4];
-        ld_group(x + e, q);
+    constexpr int G = XPre<NT>::G;
+    const uint32_t ng = nbl * 16u;
+    auto put = [&](uint32_t gi, float4 (&q)[4]) {
         if (norm) {
             float4 w[4];
-            ld_group(normw + e, w);
+            ld_group(normw + group_elem<FMT>(b0, gi), w);
             scale_group(q, inv, w);
         }
         put_group<FMT>(lds, gi, q);
+    };
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        const uint32_t gi = threadIdx.x + uint32_t(i * NT);
+        if (gi < ng) put(gi, pre.q[i]);
+    }
+    for (uint32_t gi = threadIdx.x + uint32_t(G * NT); gi < ng; gi += NT) {
+        float4 r[4];
+        ld_group(x + group_elem<FMT>(b0, gi), r);
+        put(gi, r);
     }
 }
 
@@ -590,22 +631,23 @@ __device__ __forceinline__ void st_group(float* p, const float4 (&q)[4])
 }
 
 // RMSNorm fused into the staging of the whole of x (nbl super-blocks): the
-// thread's first group of x and of the norm weights is loaded once, its
+// thread's first group of x and of the norm weights is loaded once (by
+// x_pre, ahead of the weight ring), its
 // squares enter the block-wide sum of squares (fp32, fixed order: the
 // thread's other groups first, then the first one, then the wave and
 // workgroup trees), and it is scaled and stored without a second read.
 template <int FMT, int NT>
-__device__ void stage_x_rms(float* lds, const float* __restrict__ x, uint32_t nbl, float eps,
+__device__ void stage_x_rms(float* lds, XPre<NT>& pre, const float* __restrict__ x, uint32_t nbl, float eps,
                             const float* __restrict__ normw, float* red, const uint8_t* __restrict__ erow,
                             float* __restrict__ raw_out)
 {
     const uint32_t ng = nbl * 16u, gi0 = threadIdx.x;
     const bool have = gi0 < ng;
-    float4 q0[4], w0[4];
-    if (have) {
+    float4 (&q0)[4] = pre.q[0];
+    float4 (&w0)[4] = pre.w;
+    if (have && erow) {
         const uint32_t e = group_elem<FMT>(0, gi0);
-        x_group(x, erow, e, q0);
-        ld_group(normw + e, w0);
+        emb_group(erow, e, q0);
         if (raw_out) st_group(raw_out + e, q0);
     }
     float ss = 0.0f;
@@ -859,6 +901,15 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
         if (lnext < S) advance(li, lj);
         ++lnext;
     };
+    // x first (see XPre), then the ring's first loads
+    const bool rms = (p.flags & F_NORM) && kb == 0 && nbl == p.nb;
+    const uint8_t* erow = nullptr;
+    // the embedding path exists only in the q/k/v epilogues (the first
+    // layer's projections): its code costs the other GEMVs registers
+    if constexpr (EPI == EPI_QKROPE || EPI == EPI_VSTORE)
+        if (rms && (p.flags & F_EMBED)) erow = p.emb + uint64_t(p.ctl->token) * p.nb * kQ4Bytes;
+    XPre<NT> pre;
+    x_pre<FMT, NT>(pre, p.x, kb, nbl, rms, p.normw);
 #pragma unroll
     for (int u = 0; u < PF - 1; ++u) load_next(buf[u]);
 
@@ -901,21 +952,13 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
     };
     load_ep(0);
 
-    if ((p.flags & F_NORM) && kb == 0 && nbl == p.nb) {
-        const uint8_t* erow = nullptr;
-        float* raw = nullptr;
-        // the embedding path exists only in the q/k/v epilogues (the first
-        // layer's projections): its code costs the other GEMVs registers
-        if constexpr (EPI == EPI_QKROPE || EPI == EPI_VSTORE)
-            if (p.flags & F_EMBED) {
-                erow = p.emb + uint64_t(p.ctl->token) * p.nb * kQ4Bytes;
-                if (bx == 0) raw = p.h_out;
-            }
-        stage_x_rms<FMT, NT>(lds, p.x, nbl, p.eps, p.normw, red, erow, raw);
+    if (rms) {
+        float* raw = erow && bx == 0 ? p.h_out : nullptr;
+        stage_x_rms<FMT, NT>(lds, pre, p.x, nbl, p.eps, p.normw, red, erow, raw);
     } else {
         float inv = 1.0f;
         if (p.flags & F_NORM) inv = rms_inv<NT>(p.x, p.nb * kQK, p.eps, red);
-        stage_x<FMT, NT>(lds, p.x, kb, nbl, (p.flags & F_NORM) != 0, inv, p.normw);
+        stage_x<FMT, NT>(lds, pre, p.x, kb, nbl, (p.flags & F_NORM) != 0, inv, p.normw);
     }
     __syncthreads();
 
