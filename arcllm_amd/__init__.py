@@ -22,8 +22,9 @@ LIB_PATH = os.path.join(_PKG, "libarcllm_hip.so")
 Q4_K = 12
 Q6_K = 14
 EXEC148 = 148  # Q4_K repacked as EXEC148 blocks (arc_gemv / arc_gemv_splitk only)
+Q6_K_PADDED = 214  # Q6_K blocks padded to 212 bytes (arc_q6_pad)
 QK = 256
-BLOCK_BYTES = {Q4_K: 144, Q6_K: 210}
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q6_K_PADDED: 212}
 
 ARC_OK = 0
 _STATUS = {
@@ -74,6 +75,7 @@ _SIGS = {
     "arc_event_record": [_P, _P],
     "arc_event_elapsed_ms": [_P, _P, _FP],
     "arc_dequant": [C.c_int, _P, _U32, _U32, _P, _P],
+    "arc_q6_pad": [_P, _U32, _U32, _P, _P],
     "arc_gemv": [C.c_int, _P, _U32, _U32, _P, _P, _P, _P],
     "arc_gateup_swiglu": [C.c_int, _P, _P, _U32, _U32, _P, _P, _P],
     "arc_gemv_splitk": [C.c_int, _P, _U32, _U32, _U32, _P, _P, _P, _P, _P],
@@ -331,6 +333,11 @@ def dequant(qtype: int, w, rows: int, K: int, out, stream: Optional[Stream] = No
     check(lib().arc_dequant(qtype, _ptr(w), rows, K, _ptr(out), _sp(stream)))
 
 
+def q6_pad(w, rows: int, K: int, padded, stream: Optional[Stream] = None) -> None:
+    """Write the padded (212-byte block, Q6_K_PADDED) image of a Q6_K tensor."""
+    check(lib().arc_q6_pad(_ptr(w), rows, K, _ptr(padded), _sp(stream)))
+
+
 def gemv(qtype: int, w, rows: int, K: int, x, y, bias=None, stream: Optional[Stream] = None) -> None:
     check(lib().arc_gemv(qtype, _ptr(w), rows, K, _ptr(x), _ptr(bias), _ptr(y), _sp(stream)))
 
@@ -373,7 +380,10 @@ def rmsnorm(x, w, n: int, eps: float, y, stream: Optional[Stream] = None) -> Non
 
 
 def lmhead_workspace_bytes(qtype: int, rows: int, K: int) -> int:
-    return int(lib().arc_lmhead_workspace_bytes(qtype, rows, K))
+    n = int(lib().arc_lmhead_workspace_bytes(qtype, rows, K))
+    if n == 0:
+        raise ArcError(2, f"no LM-head workspace size for qtype {qtype}, {rows} x {K}")
+    return n
 
 
 def lmhead_argmax(qtype: int, w, rows: int, K: int, h, normw, eps: float, logits, workspace, out,

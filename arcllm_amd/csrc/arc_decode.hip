@@ -433,8 +433,8 @@ static int dims_ok(const arc_model_dims& d)
                          d.hidden, d.q_heads, d.kv_heads, d.head_dim, d.ffn, d.vocab, d.layers);
     if (d.hidden / kQK > uint32_t(kPanel) || d.ffn / kQK > uint32_t(kPanel))
         return set_error(ARC_ERR_UNSUPPORTED, "hidden and ffn must be <= %d", kPanel * kQK);
-    // Q6_K tensors are read through 32-bit byte offsets
-    if (uint64_t(d.vocab) * (d.hidden / kQK) * kQ6Bytes > 0xfffffff0ull)
+    // Q6_K tensors (held padded) are read through 32-bit byte offsets
+    if (uint64_t(d.vocab) * (d.hidden / kQK) * kQ6PBytes > 0xfffffff0ull)
         return set_error(ARC_ERR_UNSUPPORTED, "output tensor of %u x %u exceeds 4 GiB", d.vocab, d.hidden);
     for (uint32_t l = 0; l < d.layers; ++l)
         if ((d.v_type[l] != kFmtQ4 && d.v_type[l] != kFmtQ6) || (d.down_type[l] != kFmtQ4 && d.down_type[l] != kFmtQ6))
@@ -449,7 +449,7 @@ int launch_lm_head(arc_session* S, const float* x, bool logits, hipStream_t st)
     const arc_model* M = S->model;
     const arc_model_dims& d = M->dims;
     const uint32_t H = d.hidden;
-    GemvParams p = make_params(kFmtQ6, M->out, nullptr, d.vocab, H, x);
+    GemvParams p = make_params(kFmtQ6P, M->out, nullptr, d.vocab, H, x);
     p.flags = F_NORM | F_ARGNEXT;
     p.normw = M->out_norm;
     p.eps = d.rms_eps;
@@ -463,11 +463,11 @@ int launch_lm_head(arc_session* S, const float* x, bool logits, hipStream_t st)
     uint32_t gx = 0;
     const bool dry = g_dry_run;
     g_dry_run = true;  // size the grid first: every workgroup needs a partials slot
-    int rc = check_hip(launch_gemv_epi(EPI_ARGMAX, kFmtQ6, c, p, 1, st, &gx), "lm head");
+    int rc = check_hip(launch_gemv_epi(EPI_ARGMAX, kFmtQ6P, c, p, 1, st, &gx), "lm head");
     g_dry_run = dry;
     if (rc) return rc;
     if (gx > S->best_cap) return set_error(ARC_ERR_UNSUPPORTED, "internal: argmax grid %u > %u", gx, S->best_cap);
-    return check_hip(launch_gemv_epi(EPI_ARGMAX, kFmtQ6, c, p, 1, st, &gx), "lm head");
+    return check_hip(launch_gemv_epi(EPI_ARGMAX, kFmtQ6P, c, p, 1, st, &gx), "lm head");
 }
 
 // Launch one decode step on the session stream (captured into a graph by the
@@ -518,7 +518,7 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
             pv.flags |= F_EMBED;
             pv.emb = M->emb;
         }
-        hipError_t e = L.v_type == kFmtQ4 ? launch_qkv<kFmtQ4>(p, pv, st) : launch_qkv<kFmtQ6>(p, pv, st);
+        hipError_t e = L.v_type == kFmtQ4 ? launch_qkv<kFmtQ4>(p, pv, st) : launch_qkv<kFmtQ6P>(p, pv, st);
         if ((rc = chk(e, "q/k/v projection"))) return rc;
 
         // attention
@@ -664,9 +664,13 @@ int arc_model_create(const arc_model_dims* dims, const void* const* tensors, arc
     // The arena: every tensor in slot order (globals, then layer by layer),
     // 256 bytes of slack after the last (kernels read 16-byte vectors past a
     // row's end), then the EXEC148 reserve.
+    // Q6_K tensors are held padded (212-byte blocks at dword boundaries, see
+    // arc_q6_pad): every Q6_K GEMV of the decode step then reads its blocks
+    // with aligned loads.
     struct Upload {
         const void* src;
-        uint64_t bytes;
+        uint64_t bytes;          // as given (GGUF layout)
+        uint64_t dev_bytes = 0;  // as held
         const void* dev = nullptr;
     };
     const size_t nt = size_t(ARC_T_GLOBAL_COUNT) + size_t(dims->layers) * ARC_T_LAYER_COUNT;
@@ -679,7 +683,8 @@ int arc_model_create(const arc_model_dims* dims, const void* const* tensors, arc
         uint32_t rows, K;
         if ((rc = arc_model_tensor_info(dims, layer, which, &qtype, &rows, &K, &up[i].bytes))) return rc;
         if (!(up[i].src = tensors[i])) return set_error(ARC_ERR_INVALID_ARGUMENT, "tensor %zu is null", i);
-        plan.place(&up[i].dev, up[i].bytes);
+        up[i].dev_bytes = qtype == kFmtQ6 ? up[i].bytes / kQ6Bytes * kQ6PBytes : up[i].bytes;
+        plan.place(&up[i].dev, up[i].dev_bytes);
         M->weight_bytes += up[i].bytes;
     }
     plan.pad(256);
@@ -692,10 +697,30 @@ int arc_model_create(const arc_model_dims* dims, const void* const* tensors, arc
     plan.pad(4096);  // nothing near the allocation's end is read past it
     M->arena_bytes = plan.bytes();
     if ((rc = plan.commit(&M->arena, "model arena"))) return rc;
-    for (const Upload& u : up)
-        if ((rc = check_hip(hipMemcpy(const_cast<void*>(u.dev), u.src, u.bytes, hipMemcpyHostToDevice),
+    std::vector<uint8_t> padded;
+    for (const Upload& u : up) {
+        const void* src = u.src;
+        if (u.dev_bytes != u.bytes) {
+            const uint64_t blocks = u.bytes / kQ6Bytes;
+            if (padded.size() < u.dev_bytes) {
+                try {
+                    padded.resize(u.dev_bytes);
+                } catch (const std::bad_alloc&) {
+                    return set_error(ARC_ERR_OUT_OF_MEMORY, "host staging for a padded Q6_K tensor");
+                }
+            }
+            const uint8_t* s8 = static_cast<const uint8_t*>(u.src);
+            for (uint64_t b = 0; b < blocks; ++b) {
+                std::memcpy(padded.data() + b * kQ6PBytes, s8 + b * kQ6Bytes, kQ6Bytes);
+                padded[b * kQ6PBytes + kQ6Bytes] = 0;
+                padded[b * kQ6PBytes + kQ6Bytes + 1] = 0;
+            }
+            src = padded.data();
+        }
+        if ((rc = check_hip(hipMemcpy(const_cast<void*>(u.dev), src, u.dev_bytes, hipMemcpyHostToDevice),
                             "upload weights")))
             return rc;
+    }
 
     auto at = [&](int layer, int which) { return up[size_t(ARC_T_GLOBAL_COUNT) + size_t(layer) * ARC_T_LAYER_COUNT + which].dev; };
     M->emb = static_cast<const uint8_t*>(up[ARC_T_TOKEN_EMBD].dev);
@@ -716,8 +741,8 @@ int arc_model_create(const arc_model_dims* dims, const void* const* tensors, arc
         L.gate = static_cast<const uint8_t*>(at(li, ARC_T_FFN_GATE));
         L.up = static_cast<const uint8_t*>(at(li, ARC_T_FFN_UP));
         L.down = static_cast<const uint8_t*>(at(li, ARC_T_FFN_DOWN));
-        L.v_type = dims->v_type[l];
-        L.down_type = dims->down_type[l];
+        L.v_type = dims->v_type[l] == kFmtQ6 ? kFmtQ6P : kFmtQ4;
+        L.down_type = dims->down_type[l] == kFmtQ6 ? kFmtQ6P : kFmtQ4;
     }
     *out = M.release();
     return ARC_OK;

@@ -12,8 +12,10 @@ constexpr int kWave = 64;
 constexpr int kQK = 256;         // weights per super-block
 constexpr int kQ4Bytes = 144;    // Q4_K super-block
 constexpr int kQ6Bytes = 210;    // Q6_K super-block
+constexpr int kQ6PBytes = 212;   // Q6_K super-block + 2 zero bytes
 constexpr int kFmtQ4 = 12;
 constexpr int kFmtQ6 = 14;
+constexpr int kFmtQ6P = 214;     // Q6_K with each 210-byte block padded to 212 (dword-aligned blocks)
 constexpr int kFmtE148 = 148;    // EXEC148: Q4_K repacked (unpacked scales, codes in element order)
 constexpr int kE148Bytes = 148;
 

@@ -161,10 +161,24 @@ __device__ __forceinline__ void q6_load(__amdgpu_buffer_rsrc_t r, uint32_t base_
     o.sh = sh;
 }
 
-// dword i of piece p of the block itself
-__device__ __forceinline__ uint32_t q6w(const Q6Blk& b, int p, int i)
+// Padded Q6_K (212-byte blocks, each at a dword boundary): the same pieces
+// read at their own addresses, nothing to realign; d is the low half of the
+// dword at 208.
+__device__ __forceinline__ void q6p_load(__amdgpu_buffer_rsrc_t r, uint32_t off, int v, Q6Blk& o)
 {
-    return __builtin_amdgcn_alignbyte(b.w[p][i + 1], b.w[p][i], b.sh);
+    const uint32_t ql = off + uint32_t(v) * 16u, qh = off + uint32_t(v & 1) * 16u;
+    const uint32_t at[5] = {ql, ql + 64u, qh + 128u, qh + 160u, off + 192u};
+#pragma unroll
+    for (int p = 0; p < 5; ++p) {
+        const u32x4v x = __builtin_amdgcn_raw_buffer_load_b128(r, at[p], 0, 0);
+        o.w[p][0] = x.x;
+        o.w[p][1] = x.y;
+        o.w[p][2] = x.z;
+        o.w[p][3] = x.w;
+        o.w[p][4] = 0u;
+    }
+    o.w[4][4] = __builtin_amdgcn_raw_buffer_load_b32(r, off + 208u, 0, 0);
+    o.sh = 0u;
 }
 
 // EXEC148 block (148 bytes, 4-byte aligned): bytes 0..3 d, dmin; 4 + 2j,
@@ -206,6 +220,11 @@ template <>
 struct BlkOf<kFmtQ4> {
     using T = Q4Blk;
     static constexpr int bytes = kQ4Bytes;
+};
+template <>
+struct BlkOf<kFmtQ6P> {
+    using T = Q6Blk;
+    static constexpr int bytes = kQ6PBytes;
 };
 template <>
 struct BlkOf<kFmtQ6> {
@@ -331,9 +350,16 @@ __device__ __forceinline__ void q4_dot(const Q4Blk (&b)[N], const float* xs, int
 // ua = low nibbles | bits (2qa, 2qa+1) of qh moved to bits 4-5, ub = high
 // nibbles | bits (2qa+4, 2qa+5); then read as fp16 subnormals u*2^-24 (the
 // staged x carries 2^24).
-template <int N>
+template <int N, bool PADDED>
 __device__ __forceinline__ void q6_dot(const Q6Blk (&b)[N], const float* xs, int v, float (&acc)[N])
 {
+    // dword i of piece p of the block itself
+    auto q6w = [](const Q6Blk& bb, int p, int i) -> uint32_t {
+        if constexpr (PADDED)
+            return bb.w[p][i];
+        else
+            return __builtin_amdgcn_alignbyte(bb.w[p][i + 1], bb.w[p][i], bb.sh);
+    };
     const int qa = v >> 1;
     const uint32_t s1 = 4u - 2u * qa, s2 = 2u * qa;
     float a[N][4];
@@ -363,7 +389,7 @@ __device__ __forceinline__ void q6_dot(const Q6Blk (&b)[N], const float* xs, int
         t = __builtin_fmaf(float(int8_t(uint8_t(q6w(b[n], 4, 1) >> i0))), __builtin_fmaf(-32.0f, S.y, a[n][1]), t);
         t = __builtin_fmaf(float(int8_t(uint8_t(q6w(b[n], 4, 2) >> i0))), __builtin_fmaf(-32.0f, S.z, a[n][2]), t);
         t = __builtin_fmaf(float(int8_t(uint8_t(q6w(b[n], 4, 3) >> i0))), __builtin_fmaf(-32.0f, S.w, a[n][3]), t);
-        const uint32_t d = b[n].w[4][4] >> (8u * b[n].sh);  // bytes 208, 209 in the low half
+        const uint32_t d = PADDED ? b[n].w[4][4] : b[n].w[4][4] >> (8u * b[n].sh);  // bytes 208, 209 in the low half
         acc[n] = fmix(d, false, t, acc[n]);  // + d * t
     }
 }
@@ -445,7 +471,7 @@ __device__ __forceinline__ void blk_dot(const typename BlkOf<FMT>::T (&b)[N], co
     else if constexpr (FMT == kFmtE148)
         e148_dot<N>(b, xs, acc);
     else
-        q6_dot<N>(b, xs, v, acc);
+        q6_dot<N, FMT == kFmtQ6P>(b, xs, v, acc);
 }
 
 // Q4_K and EXEC148 blocks (16- and 4-byte aligned) are read through their
@@ -793,7 +819,7 @@ __device__ void argmax_finish(const GemvParams& p, uint32_t n)
 template <int FMT, int EPI>
 constexpr int ring_depth()
 {
-    return FMT == kFmtQ4 ? ARC_PF_Q4 : FMT == kFmtQ6 ? ARC_PF_Q6 : ARC_PF_E148;
+    return FMT == kFmtQ4 ? ARC_PF_Q4 : (FMT == kFmtQ6 || FMT == kFmtQ6P) ? ARC_PF_Q6 : ARC_PF_E148;
 }
 static_assert(ARC_PF_Q4 >= 2 && ARC_PF_Q6 >= 2 && ARC_PF_E148 >= 2, "a ring holds at least two buffers");
 
@@ -835,10 +861,11 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
     const uint32_t S = my_tiles * nj;
 
     auto tile_row = [&](uint32_t tile, int j) { return tile * kTileRows + rg * RPL + j; };
-    // Q6_K: a buffer descriptor over each matrix (the host keeps a Q6_K
-    // tensor below 4 GiB); unused, and removed, for the other formats
-    // (descriptor bases at the dword boundary at or below each tensor; the
-    // last block's final dword holds 2 bytes past the tensor, hence + 4)
+    // Q6_K and padded Q6_K: a buffer descriptor over each matrix (the host
+    // keeps such a tensor below 4 GiB); unused, and removed, for the other
+    // formats (descriptor bases at the dword boundary at or below each tensor,
+    // where a padded tensor starts; a Q6_K block's final dword holds 2 bytes
+    // past the tensor, hence + 4)
     const uint32_t rows0 = EPI == EPI_QKROPE ? p.row_split : p.rows;
     const uint8_t* w1 = NMAT == 2 || EPI == EPI_QKROPE ? p.w1 : p.w0;
     const uint32_t sh0 = uint32_t(reinterpret_cast<uintptr_t>(p.w0)) & 3u;
@@ -857,7 +884,17 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
 #pragma unroll
             for (int r = 0; r < RPL; ++r) {
                 const uint32_t row = min(tile_row(tile, r), p.rows - 1);  // clamp: result discarded
-                if constexpr (FMT == kFmtQ6) {
+                if constexpr (FMT == kFmtQ6P) {
+                    const uint32_t col = (kb + bl) * uint32_t(kBB);
+                    if constexpr (EPI == EPI_QKROPE) {
+                        if (row < p.row_split)
+                            q6p_load(q6r0, row * uint32_t(p.row_bytes) + col, v, b[m * RPL + r]);
+                        else
+                            q6p_load(q6r1, (row - p.row_split) * uint32_t(p.row_bytes) + col, v, b[m * RPL + r]);
+                    } else {
+                        q6p_load(m == 0 ? q6r0 : q6r1, row * uint32_t(p.row_bytes) + col, v, b[m * RPL + r]);
+                    }
+                } else if constexpr (FMT == kFmtQ6) {
                     const uint32_t col = (kb + bl) * uint32_t(kBB);
                     if constexpr (EPI == EPI_QKROPE) {
                         if (row < p.row_split)
@@ -1198,7 +1235,7 @@ inline thread_local int g_force_waves = 0;
 template <int FMT>
 constexpr bool layout_built(int rpl)
 {
-    return !(FMT == kFmtQ6 && rpl == 4);
+    return !((FMT == kFmtQ6 || FMT == kFmtQ6P) && rpl == 4);
 }
 
 template <int FMT, int EPI>
@@ -1275,6 +1312,7 @@ template <int EPI>
 hipError_t launch_gemv(int qtype, const Cfg& c, const GemvParams& p, uint32_t splits, hipStream_t s, uint32_t* gx)
 {
     if (qtype == kFmtQ4) return launch_cfg<kFmtQ4, EPI>(c, p, splits, s, gx);
+    if (qtype == kFmtQ6P) return launch_cfg<kFmtQ6P, EPI>(c, p, splits, s, gx);
     if (qtype == kFmtE148) {
         // EXEC148 is the down projection's representation: plain and split-K only
         if constexpr (EPI == EPI_PLAIN || EPI == EPI_PARTIAL || EPI == EPI_COLPART)
@@ -1296,11 +1334,14 @@ inline hipError_t launch_gemv_epi(int epi, int qtype, const Cfg& c, const GemvPa
     }
 }
 
-static int block_bytes(int qtype) { return qtype == kFmtQ4 ? kQ4Bytes : qtype == kFmtE148 ? kE148Bytes : kQ6Bytes; }
+static int block_bytes(int qtype)
+{
+    return qtype == kFmtQ4 ? kQ4Bytes : qtype == kFmtE148 ? kE148Bytes : qtype == kFmtQ6P ? kQ6PBytes : kQ6Bytes;
+}
 
 static int check_shape(int qtype, const void* w, uint32_t rows, uint32_t K)
 {
-    if (qtype != kFmtQ4 && qtype != kFmtQ6 && qtype != kFmtE148)
+    if (qtype != kFmtQ4 && qtype != kFmtQ6 && qtype != kFmtQ6P && qtype != kFmtE148)
         return set_error(ARC_ERR_UNSUPPORTED, "unsupported qtype %d", qtype);
     if (!w) return set_error(ARC_ERR_INVALID_ARGUMENT, "null weight pointer");
     if (rows == 0 || K == 0 || (K % kQK) != 0)
@@ -1312,6 +1353,9 @@ static int check_shape(int qtype, const void* w, uint32_t rows, uint32_t K)
     if (qtype == kFmtQ6 && uint64_t(rows) * (K / kQK) * kQ6Bytes > 0xfffffff0ull)
         return set_error(ARC_ERR_UNSUPPORTED, "Q6_K tensor of %u x %u exceeds 4 GiB", rows, K);
     if (qtype == kFmtE148 && (a & 3u)) return set_error(ARC_ERR_INVALID_ARGUMENT, "EXEC148 tensor not 4-byte aligned");
+    if (qtype == kFmtQ6P && (a & 3u)) return set_error(ARC_ERR_INVALID_ARGUMENT, "padded Q6_K tensor not 4-byte aligned");
+    if (qtype == kFmtQ6P && uint64_t(rows) * (K / kQK) * kQ6PBytes > 0xfffffff0ull)
+        return set_error(ARC_ERR_UNSUPPORTED, "padded Q6_K tensor of %u x %u exceeds 4 GiB", rows, K);
     return ARC_OK;
 }
 

@@ -154,12 +154,14 @@ __global__ __launch_bounds__(256) void k_dequant_q4(const uint8_t* __restrict__ 
     out[blk * kQK + k] = t1 - t2;
 }
 
-__global__ __launch_bounds__(256) void k_dequant_q6(const uint8_t* __restrict__ w, float* __restrict__ out)
+// stride: kQ6Bytes, or kQ6PBytes for padded Q6_K
+__global__ __launch_bounds__(256) void k_dequant_q6(const uint8_t* __restrict__ w, uint32_t stride,
+                                                    float* __restrict__ out)
 {
 #pragma clang fp contract(off)
     const uint64_t blk = blockIdx.x;
     const uint32_t k = threadIdx.x;
-    const uint8_t* b = w + blk * kQ6Bytes;
+    const uint8_t* b = w + blk * stride;
     const uint32_t half = k >> 7, kk = k & 127u, l = kk & 31u, quarter = kk >> 5;
     const uint8_t* ql = b + half * 64u;
     const uint8_t* qh = b + 128u + half * 32u;
@@ -172,6 +174,23 @@ __global__ __launch_bounds__(256) void k_dequant_q6(const uint8_t* __restrict__ 
     const float d = f16_bits_to_f32(uint32_t(b[208]) | (uint32_t(b[209]) << 8));
     const float t0 = d * float(scale);
     out[blk * kQK + k] = t0 * float(q);
+}
+
+// Padded Q6_K: thread t writes dword t % 53 of block t / 53 (bytes 4j .. 4j+3
+// of the 210-byte source block, read as two halves: the source is 2-byte
+// aligned); dword 52 is bytes 208, 209 and two zero bytes.
+constexpr uint32_t kQ6PDwords = kQ6PBytes / 4;
+static_assert(kQ6PBytes == kQ6Bytes + 2 && kQ6PBytes % 4 == 0, "one 2-byte pad per block");
+__global__ __launch_bounds__(256) void k_q6_pad(const uint16_t* __restrict__ src, uint32_t* __restrict__ dst,
+                                                uint64_t dwords)
+{
+    const uint64_t t = uint64_t(blockIdx.x) * 256u + threadIdx.x;
+    if (t >= dwords) return;
+    const uint64_t blk = t / kQ6PDwords;
+    const uint32_t j = uint32_t(t % kQ6PDwords);
+    const uint16_t* b = src + blk * (kQ6Bytes / 2) + 2u * j;
+    const uint32_t lo = b[0], hi = j + 1u < kQ6PDwords ? uint32_t(b[1]) : 0u;
+    dst[t] = lo | (hi << 16);
 }
 
 }  // namespace arc
@@ -221,8 +240,25 @@ int arc_dequant(int qtype, const void* w, uint32_t rows, uint32_t K, float* out,
     if (qtype == kFmtQ4)
         hipLaunchKernelGGL(k_dequant_q4, dim3(uint32_t(blocks)), dim3(256), 0, s, static_cast<const uint8_t*>(w), out);
     else
-        hipLaunchKernelGGL(k_dequant_q6, dim3(uint32_t(blocks)), dim3(256), 0, s, static_cast<const uint8_t*>(w), out);
+        hipLaunchKernelGGL(k_dequant_q6, dim3(uint32_t(blocks)), dim3(256), 0, s, static_cast<const uint8_t*>(w),
+                           uint32_t(qtype == kFmtQ6P ? kQ6PBytes : kQ6Bytes), out);
     return check_hip(hipGetLastError(), "dequant launch");
+}
+
+int arc_q6_pad(const void* q6, uint32_t rows, uint32_t K, void* padded, arc_stream_t stream)
+{
+    int rc = check_shape(kFmtQ6, q6, rows, K);
+    if (rc) return rc;
+    if ((rc = check_shape(kFmtQ6P, padded, rows, K))) return rc;
+    const uint64_t blocks = uint64_t(rows) * (K / kQK);
+    const uint8_t* a = static_cast<const uint8_t*>(q6);
+    const uint8_t* b = static_cast<const uint8_t*>(padded);
+    if (b < a + blocks * kQ6Bytes && a < b + blocks * kQ6PBytes)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "padded image overlaps its source");
+    const uint64_t dwords = blocks * kQ6PDwords;
+    hipLaunchKernelGGL(k_q6_pad, dim3(uint32_t((dwords + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(q6), static_cast<uint32_t*>(padded), dwords);
+    return check_hip(hipGetLastError(), "Q6_K pad launch");
 }
 
 int arc_gemv(int qtype, const void* w, uint32_t rows, uint32_t K, const float* x, const float* bias, float* y,
@@ -305,7 +341,7 @@ static uint32_t lm_max_wgs(uint32_t rows) { return min((rows + 3u) / 4u, uint32_
 
 size_t arc_lmhead_workspace_bytes(int qtype, uint32_t rows, uint32_t K)
 {
-    if ((qtype != kFmtQ4 && qtype != kFmtQ6) || rows == 0 || K == 0 || K % kQK) return 0;
+    if ((qtype != kFmtQ4 && qtype != kFmtQ6 && qtype != kFmtQ6P) || rows == 0 || K == 0 || K % kQK) return 0;
     return size_t(lm_max_wgs(rows)) * sizeof(ArgBest);
 }
 

@@ -109,6 +109,17 @@ struct WDec<kFmtQ6> {
     u32x4 ql[4], qh[2];
     float f[8], n[8];
 };
+// Padded Q6_K (the model's Q6_K tensors): the same block bytes at a dword
+// boundary, so load_w reads them with sh = 0; only the block stride differs.
+template <>
+struct WRaw<kFmtQ6P> : WRaw<kFmtQ6> {};
+template <>
+struct WDec<kFmtQ6P> : WDec<kFmtQ6> {};
+template <int FMT>
+constexpr int pf_block_bytes()
+{
+    return FMT == kFmtQ4 ? kQ4Bytes : FMT == kFmtQ6P ? kQ6PBytes : kQ6Bytes;
+}
 
 template <int FMT>
 __device__ __forceinline__ void load_w(const uint8_t* blk, uint32_t kh, WRaw<FMT>& r)
@@ -448,7 +459,7 @@ __global__ __launch_bounds__(512, 1) void k_pf_gemm_gu(PfGemm p)
 {
     extern __shared__ __align__(16) _Float16 ash[];  // [2][MB*32][kPfLd]
     constexpr int kStage = MB * 32 * kPfLd;
-    constexpr int kBB = FMT == kFmtQ4 ? kQ4Bytes : kQ6Bytes;
+    constexpr int kBB = pf_block_bytes<FMT>();
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t part = uint32_t(wave) >> 2, kh = uint32_t(lane) >> 5;
     const uint32_t c = uint32_t(wave & 3) * 32 + uint32_t(lane & 31);  // column within the tile
@@ -531,7 +542,7 @@ __device__ __forceinline__ void pf_gemm_body(const PfGemm& p, uint32_t tile)
     static_assert(!SWIGLU || NF == 2, "SwiGLU pairs a gate and an up row per lane");
     extern __shared__ __align__(16) _Float16 ash[];  // [2][MB*32][kPfLd]
     constexpr int kStage = MB * 32 * kPfLd;
-    constexpr int kBB = FMT == kFmtQ4 ? kQ4Bytes : kQ6Bytes;
+    constexpr int kBB = pf_block_bytes<FMT>();
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t kh = uint32_t(lane) >> 5;
 
@@ -1020,7 +1031,7 @@ hipError_t launch_qkv_mb(const PfGemm& qk, const PfGemm& v, uint32_t mb, uint32_
 
 hipError_t launch_qkv(const PfGemm& qk, const PfGemm& v, int vtype, uint32_t mb, uint32_t splits, hipStream_t st)
 {
-    return vtype == kFmtQ4 ? launch_qkv_mb<kFmtQ4>(qk, v, mb, splits, st) : launch_qkv_mb<kFmtQ6>(qk, v, mb, splits, st);
+    return vtype == kFmtQ4 ? launch_qkv_mb<kFmtQ4>(qk, v, mb, splits, st) : launch_qkv_mb<kFmtQ6P>(qk, v, mb, splits, st);
 }
 
 uint32_t m_blocks(uint32_t M)
@@ -1148,7 +1159,7 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             g.tiles = (g.N + 127) / 128;
             PfGemm gv = g;
             gv.w0 = gv.w1 = L.v;
-            gv.row_bytes = uint64_t(g.nb) * (L.v_type == kFmtQ4 ? kQ4Bytes : kQ6Bytes);
+            gv.row_bytes = uint64_t(g.nb) * (L.v_type == kFmtQ4 ? kQ4Bytes : kQ6PBytes);
             gv.ncol0 = kvd;
             gv.N = kvd;
             gv.out = pf->part + (H + kvd);
@@ -1190,14 +1201,14 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
             dn.ldx = F;
             dn.nb = F / kQK;
             dn.w0 = dn.w1 = L.down;
-            dn.row_bytes = uint64_t(dn.nb) * (L.down_type == kFmtQ4 ? kQ4Bytes : kQ6Bytes);
+            dn.row_bytes = uint64_t(dn.nb) * (L.down_type == kFmtQ4 ? kQ4Bytes : kQ6PBytes);
             dn.ncol0 = H;
             dn.N = H;
             dn.ldo = H;
             split_plan(dn.N, dn.nb, gx, sp, bps);
             dn.bps = bps;
             rc = chk(L.down_type == kFmtQ4 ? launch_gemm_mb<kFmtQ4, 1, false>(dn, mb, gx, sp, st)
-                                           : launch_gemm_mb<kFmtQ6, 1, false>(dn, mb, gx, sp, st),
+                                           : launch_gemm_mb<kFmtQ6P, 1, false>(dn, mb, gx, sp, st),
                      "down projection");
             if (rc) return rc;
             if (l + 1 < d.layers) {

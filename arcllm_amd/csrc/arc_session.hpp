@@ -91,7 +91,7 @@ inline uint64_t exec148_image_bytes(uint32_t rows, uint32_t K) { return uint64_t
 struct Layer {
     const uint8_t *q, *k, *v, *o, *gate, *up, *down;
     const float *attn_norm, *ffn_norm, *qb, *kb, *vb;
-    int v_type, down_type;
+    int v_type, down_type;  // kFmtQ4, or kFmtQ6P: the model holds Q6_K tensors padded
 };
 
 }  // namespace arc

@@ -48,8 +48,14 @@ typedef enum arc_status {
 typedef enum arc_qtype {
     ARC_Q4_K = 12,     /* ggml type id of Q4_K (src/arcllm_v1_runtime.cpp:168) */
     ARC_Q6_K = 14,     /* ggml type id of Q6_K */
-    ARC_EXEC148 = 148  /* Q4_K repacked as EXEC148 (src/q4_down_exec148_materializer.h:14-17):
+    ARC_EXEC148 = 148, /* Q4_K repacked as EXEC148 (src/q4_down_exec148_materializer.h:14-17):
                           accepted by arc_gemv and arc_gemv_splitk */
+    ARC_Q6_K_PADDED = 214 /* Q6_K with 2 zero bytes after each 210-byte block, so every
+                             block starts at a dword boundary (written by arc_q6_pad; the
+                             model arena holds its Q6_K tensors this way).  Accepted by
+                             arc_dequant, arc_gemv, arc_gemv_splitk and arc_lmhead_argmax.
+                             No counterpart in the reference: a device-side layout of
+                             the same blocks, for dword-aligned loads. */
 } arc_qtype;
 
 typedef void *arc_stream_t; /* a hipStream_t; NULL is the default stream */
@@ -92,6 +98,13 @@ int arc_event_elapsed_ms(arc_event_t start, arc_event_t stop, float *ms);
  * each product/difference rounded separately, left to right. */
 int arc_dequant(int qtype, const void *w, uint32_t rows, uint32_t K, float *out,
                 arc_stream_t stream);
+
+/* Padded image of a Q6_K tensor (rows x K; device pointers, q6 2-byte and
+ * padded 4-byte aligned, not overlapping): rows*(K/256) blocks of 212 bytes,
+ * each the 210-byte block followed by two zero bytes.  No counterpart in the
+ * reference (it reads GGUF blocks in place): the loads of a padded block
+ * are dword-aligned, which the Q6_K GEMVs run faster on. */
+int arc_q6_pad(const void *q6, uint32_t rows, uint32_t K, void *padded, arc_stream_t stream);
 
 /* ------------------------------------------------------------------ GEMV */
 /* y[r] = sum_k w[r,k] * x[k] (+ bias[r] when bias != NULL), fp32 accumulate.
@@ -153,7 +166,8 @@ int arc_exec148_validate_many(const void *const *q4, const void *const *exec, ui
 int arc_rmsnorm(const float *x, const float *w, uint32_t n, float eps, float *y,
                 arc_stream_t stream);
 
-/* Bytes of device workspace arc_lmhead_argmax needs for `rows` vocabulary rows. */
+/* Bytes of device workspace arc_lmhead_argmax needs for `rows` vocabulary
+ * rows; 0 for a qtype or shape the LM head does not take. */
 size_t arc_lmhead_workspace_bytes(int qtype, uint32_t rows, uint32_t K);
 
 /* Greedy LM-head step on the GPU: x = RMSNorm(h; normw, eps), logits =
@@ -319,8 +333,9 @@ uint32_t arc_session_kernels_per_step(const arc_session *session);
 
 /* Device pointer of a model tensor (layer < 0: the global tensors
  * ARC_T_TOKEN_EMBD .. ARC_T_OUTPUT_NORM; otherwise slot `which` of `layer`),
- * in the layout of arc_model_create.  Used by the Q4_K FFN-down backend to
- * build the EXEC148 representation on the GPU. */
+ * in the layout of arc_model_create, except that Q6_K tensors are held as
+ * ARC_Q6_K_PADDED.  Used by the Q4_K FFN-down backend to build the EXEC148
+ * representation on the GPU. */
 int arc_model_tensor_device(const arc_model *model, int layer, int which, const void **ptr);
 
 /* Route B of the Q4_K FFN-down capability for one decode layer: the decode

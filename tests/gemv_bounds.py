@@ -20,8 +20,8 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-Q4, Q6, E148 = 12, 14, 148
-BLOCK_BYTES = {Q4: 144, Q6: 210, E148: 148}
+Q4, Q6, E148, Q6P = 12, 14, 148, 214
+BLOCK_BYTES = {Q4: 144, Q6: 210, E148: 148, Q6P: 212}
 KQK, XBLK, SLOT, WAVE = 256, 272, 68, 64
 PLAIN, SWIGLU, PARTIAL, ARGMAX, COLPART, QKROPE, VSTORE = range(7)
 RING = 2  # ARC_PF_Q4 / ARC_PF_Q6 / ARC_PF_E148 (ring_depth)
@@ -82,13 +82,18 @@ def x_group_offset(fmt, v, t):
 
 def block_reads(fmt, v, blk_off, tensor_align):
     """Byte ranges [lo, hi) of one lane's block loads, relative to the tensor
-    base (q4_load, e148_load, q6_load)."""
+    base (q4_load, e148_load, q6_load, q6p_load)."""
     if fmt == Q4:
         return [(blk_off, blk_off + 4), (blk_off + 4, blk_off + 16), (blk_off + 16 + v * 16, blk_off + 32 + v * 16),
                 (blk_off + 80 + v * 16, blk_off + 96 + v * 16)]
     if fmt == E148:
         return [(blk_off, blk_off + 4), (blk_off + 4 + 4 * v, blk_off + 8 + 4 * v),
                 (blk_off + 20 + 32 * v, blk_off + 36 + 32 * v), (blk_off + 36 + 32 * v, blk_off + 52 + 32 * v)]
+    if fmt == Q6P:
+        # padded Q6_K: the five 16-byte pieces at their own (dword) addresses
+        # and the dword at 208 holding d
+        return [(blk_off + o, blk_off + o + 16) for o in (v * 16, 64 + v * 16, 128 + (v & 1) * 16, 160 + (v & 1) * 16,
+                                                           192 + 0 * v)] + [(blk_off + 208 + 0 * v, blk_off + 212 + 0 * v)]
     # Q6_K: a dwordx4 plus the following dword from the dword boundary at or
     # below each piece (the descriptor base sits at that boundary too)
     sh = (blk_off + tensor_align) & 3
@@ -118,7 +123,7 @@ def simulate(c: Config, mistake: str | None = None) -> Report:
     # tensor bytes per matrix (QKROPE: w0 has row_split rows, w1 the rest)
     mat_rows = [c.row_split, c.rows - c.row_split] if c.epi == QKROPE else [c.rows] * nmat
     mat_bytes = [r * row_bytes for r in mat_rows]
-    if c.fmt == Q6:
+    if c.fmt in (Q6, Q6P):
         lo_ok = -c.tensor_align
         hi_ok = [b + 4 for b in mat_bytes]  # the descriptor's range (tensor_rsrc)
     else:
@@ -247,4 +252,4 @@ def simulate(c: Config, mistake: str | None = None) -> Report:
 def built_layouts(fmt):
     """The (bs, rpl) layouts launch_cfg instantiates (layout_built)."""
     lay = [(1, 1), (1, 2), (1, 4), (2, 1), (2, 2), (2, 4), (4, 1), (4, 2), (8, 1), (8, 2), (16, 1)]
-    return [(b, r) for b, r in lay if not (fmt == Q6 and r == 4)]
+    return [(b, r) for b, r in lay if not (fmt in (Q6, Q6P) and r == 4)]

@@ -87,8 +87,14 @@ def test_error_raises_arcerror():
 
 def test_lmhead_workspace_bytes():
     assert arc.lmhead_workspace_bytes(14, 152064, 3584) >= 16 * (152064 // 16)
-    assert arc.lmhead_workspace_bytes(14, 0, 3584) == 0
-    assert arc.lmhead_workspace_bytes(14, 10, 300) == 0
+    assert arc.lmhead_workspace_bytes(arc.Q6_K_PADDED, 152064, 3584) == arc.lmhead_workspace_bytes(14, 152064, 3584)
+    # the C function answers 0 for what the LM head does not take; the binding raises
+    assert arc.lib().arc_lmhead_workspace_bytes(14, 0, 3584) == 0
+    assert arc.lib().arc_lmhead_workspace_bytes(14, 10, 300) == 0
+    assert arc.lib().arc_lmhead_workspace_bytes(148, 10, 3584) == 0
+    for bad in ((14, 0, 3584), (14, 10, 300), (148, 10, 3584)):
+        with pytest.raises(arc.ArcError):
+            arc.lmhead_workspace_bytes(*bad)
 
 
 def test_synth_packed_deterministic_and_distributed():

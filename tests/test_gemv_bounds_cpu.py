@@ -31,7 +31,7 @@ def run(c, mistake=None):
 
 
 def cases():
-    for fmt in (gb.Q4, gb.Q6, gb.E148):
+    for fmt in (gb.Q4, gb.Q6, gb.E148, gb.Q6P):
         for (bs, rpl), W, (rows, K) in itertools.product(gb.built_layouts(fmt), (4, 8), SHAPES):
             nb = K // 256
             yield gb.Config(fmt, bs, rpl, gb.PLAIN, W, rows, K, tensor_align=2 if fmt == gb.Q6 else 0)
@@ -74,8 +74,9 @@ def test_qkrope_and_vstore_epilogues_stay_in_bounds():
         c = gb.Config(fmt, 4, 2, gb.QKROPE, 4, 3584 + 512, 3584, row_split=3584, kv_dim=512, pos=700, max_ctx=701)
         for gx, r in run(c):
             assert not r.violations, (gx, r.violations)
-    for fmt in (gb.Q4, gb.Q6):
-        c = gb.Config(fmt, 4, 1, gb.VSTORE, 4, 512, 3584, kv_dim=512, pos=0, max_ctx=1, tensor_align=2)
+    for fmt in (gb.Q4, gb.Q6, gb.Q6P):
+        c = gb.Config(fmt, 4, 1, gb.VSTORE, 4, 512, 3584, kv_dim=512, pos=0, max_ctx=1,
+                      tensor_align=2 if fmt == gb.Q6 else 0)
         for gx, r in run(c):
             assert not r.violations, (gx, r.violations)
 

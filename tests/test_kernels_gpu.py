@@ -396,3 +396,60 @@ def test_every_layout_fused_splitk_lmhead(bs, rpl):
     ref = orc.gemv_r64(arc.Q6_K, wl, rows, K, x)
     assert orc.rel_err(logits, ref) <= TOL
     assert tok == int(np.argmax(ref)) and nf == 0
+
+
+def _pad_q6(w, rows, K):
+    b = np.asarray(w, np.uint8).reshape(rows * (K // 256), 210)
+    out = np.zeros((b.shape[0], 212), np.uint8)
+    out[:, :210] = b
+    return out.ravel()
+
+
+@pytest.mark.parametrize("rows,K", [(1, 256), (37, 768), (3584, 18944)])
+def test_q6_pad_image(rows, K):
+    """arc_q6_pad writes each 210-byte block followed by two zero bytes, from
+    a source that starts 2 bytes past a dword boundary too."""
+    w = packed(arc.Q6_K, rows, K, 80)
+    src = arc.DeviceBuffer(w.size + 2)
+    src.upload(np.concatenate([np.zeros(2, np.uint8), w]))
+    img = arc.DeviceBuffer(rows * (K // 256) * 212)
+    arc.check(arc.lib().arc_q6_pad(src.ptr + 2, rows, K, img.ptr, None))
+    arc.synchronize()
+    assert np.array_equal(img.download(np.uint8), _pad_q6(w, rows, K))
+
+
+@pytest.mark.parametrize("rows,K", [(37, 512), (1000, 3584), (3584, 18944)])
+def test_padded_q6_gemv_and_dequant_bit_identical(rows, K):
+    """The padded layout (the model's Q6_K tensors) gives the same bits as the
+    GGUF layout: dequant, plain GEMV with bias, split-K with residual."""
+    w = packed(arc.Q6_K, rows, K, 81)
+    wp = _pad_q6(w, rows, K)
+    x = dev(arc.synth_normal(SEED, 82, K))
+    bias = dev(arc.synth_normal(SEED, 83, rows))
+    d1, d2 = arc.DeviceBuffer(rows * K * 4), arc.DeviceBuffer(rows * K * 4)
+    arc.dequant(arc.Q6_K, dev(w), rows, K, d1)
+    arc.dequant(arc.Q6_K_PADDED, dev(wp), rows, K, d2)
+    assert same_bits(d1.download(np.float32), d2.download(np.float32))
+    y1, y2 = arc.DeviceBuffer(rows * 4), arc.DeviceBuffer(rows * 4)
+    arc.gemv(arc.Q6_K, dev(w), rows, K, x, y1, bias=bias)
+    arc.gemv(arc.Q6_K_PADDED, dev(wp), rows, K, x, y2, bias=bias)
+    assert same_bits(y1.download(np.float32), y2.download(np.float32))
+    ref = orc.gemv_r64(arc.Q6_K, w, rows, K, arc.synth_normal(SEED, 82, K))
+    assert orc.rel_err(y2.download(np.float32) - bias.download(np.float32), ref) <= TOL
+    nb = K // 256
+    splits = min(nb, 74)
+    part = arc.DeviceBuffer(splits * rows * 4)
+    res = dev(arc.synth_normal(SEED, 84, rows))
+    arc.gemv_splitk(arc.Q6_K, dev(w), rows, K, splits, x, part, y1, residual=res)
+    arc.gemv_splitk(arc.Q6_K_PADDED, dev(wp), rows, K, splits, x, part, y2, residual=res)
+    assert same_bits(y1.download(np.float32), y2.download(np.float32))
+
+
+def test_padded_q6_lmhead_bit_identical():
+    rows, K = 30000, 3584
+    w = packed(arc.Q6_K, rows, K, 85)
+    h = arc.synth_normal(SEED, 86, K)
+    nw = arc.synth_normal(SEED, 87, K, 1.0, 0.05)
+    t1, n1, l1 = _lmhead(arc.Q6_K, dev(w), rows, K, h, nw)
+    t2, n2, l2 = _lmhead(arc.Q6_K_PADDED, dev(_pad_q6(w, rows, K)), rows, K, h, nw)
+    assert (t1, n1) == (t2, n2) and same_bits(l1, l2)
