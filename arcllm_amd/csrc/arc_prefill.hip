@@ -128,6 +128,16 @@ __device__ __forceinline__ void load_w(const uint8_t* blk, uint32_t kh, WRaw<FMT
         r.hdr = *reinterpret_cast<const u32x4*>(blk);
 #pragma unroll
         for (int c = 0; c < 4; ++c) r.qs[c] = *reinterpret_cast<const u32x4*>(blk + 16 + c * 32 + kh * 16);
+    } else if constexpr (FMT == kFmtQ6P) {
+        // padded block at a dword boundary: the pieces as they are
+#pragma unroll
+        for (int i = 0; i < 7; ++i) {
+            const uint32_t o = i < 4 ? uint32_t(i) * 32u + kh * 16u : i < 6 ? 128u + uint32_t(i - 4) * 32u + kh * 16u : 192u;
+            r.v[i] = *reinterpret_cast<const u32x4a4*>(blk + o);
+            r.e[i] = 0u;
+        }
+        r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
+        r.sh = 0u;
     } else {
         // every dword read lies inside the 210-byte block: a piece at offset o
         // reads [o - sh, o - sh + 20) when sh = 2 and [o, o + 16) plus the
@@ -175,6 +185,10 @@ __device__ __forceinline__ void decode_w(const WRaw<FMT>& r, uint32_t kh, WDec<F
         u32x4 al[7];
 #pragma unroll
         for (int i = 0; i < 7; ++i) {
+            if constexpr (FMT == kFmtQ6P) {
+                al[i] = r.v[i];
+                continue;
+            }
             al[i].x = __builtin_amdgcn_alignbyte(r.v[i].y, r.v[i].x, r.sh);
             al[i].y = __builtin_amdgcn_alignbyte(r.v[i].z, r.v[i].y, r.sh);
             al[i].z = __builtin_amdgcn_alignbyte(r.v[i].w, r.v[i].z, r.sh);
