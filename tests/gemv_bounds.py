@@ -154,6 +154,21 @@ def simulate(c: Config, mistake: str | None = None) -> Report:
         rep.check("x staging LDS store", dst, dst + 16, 0, panel * XBLK)
         sdst = (gi >> 4) * XBLK + ((gi >> 2) & 3) * SLOT + 64 + (gi & 3)
         rep.check("x group-sum LDS store", sdst, sdst + 1, 0, panel * XBLK)
+        # x_pre: each thread's groups loaded ahead of the ring, indices clamped
+        # into the panel (8-wave launches: all groups of an 80-block panel;
+        # 4-wave: the first), and with the fused norm its first group of the
+        # norm weights
+        NT = W * WAVE
+        G = -(-(80 * 16) // NT) if NT >= 512 else 1
+        t = np.arange(NT)
+        for i in range(G):
+            gp = np.minimum(t + i * NT, nbl * 16 - 1)
+            ep = (kb + (gp >> 4)) * KQK + x_group_offset(c.fmt, (gp >> 2) & 3, gp & 3)
+            rep.check("x pre-load", ep, ep + 16, 0, nb * KQK)
+        if kb == 0 and nbl == nb:
+            gp = np.minimum(t, nbl * 16 - 1)
+            ep = (gp >> 4) * KQK + x_group_offset(c.fmt, (gp >> 2) & 3, gp & 3)
+            rep.check("norm weight pre-load", ep, ep + 16, 0, nb * KQK)
 
         for bx in range(gx):
             for wave in range(W):
