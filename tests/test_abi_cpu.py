@@ -69,6 +69,12 @@ def test_version_and_device_count_without_gpu_is_not_an_error():
         lambda L: L.arc_gemv_splitk(14, 16, 8, 512, 0, 16, 16, None, 16, None),  # zero splits
         lambda L: L.arc_lmhead_argmax(14, 16, 8, 512, 16, None, 1e-6, None, None, 16, None),  # no workspace
         lambda L: L.arc_dequant(12, 16, 8, 100, 16, None),
+        lambda L: L.arc_gemv(214, 18, 8, 256, 16, None, 16, None),  # padded Q6_K base not 4-aligned
+        lambda L: L.arc_q6_pad(None, 8, 256, 16, None),  # null source
+        lambda L: L.arc_q6_pad(17, 8, 256, 4096, None),  # Q6_K source odd
+        lambda L: L.arc_q6_pad(16, 8, 256, 4098, None),  # padded image not 4-aligned
+        lambda L: L.arc_q6_pad(4096, 8, 256, 4096 + 210, None),  # image overlaps its source
+        lambda L: L.arc_q6_pad(16, 8, 300, 4096, None),  # K not a multiple of 256
         lambda L: L.arc_tune_force(3, 1),
     ],
 )
