@@ -1,8 +1,9 @@
 """The bounds model of the packed GEMV (tests/gemv_bounds.py) over the
-launchable layouts and epilogues, over grids from one workgroup to one wave
-tile per wave, and over the Q6_K layouts with four rows per lane that the
-library refuses to launch (one of them, k_gemv<Q6_K, 2, 4, PLAIN, 4>, took a
-GPU memory fault once at 301 x 3584): every weight read, epilogue load, x
+launchable layouts and epilogues of Q4_K, Q6_K (GGUF and padded 212-byte
+blocks) and EXEC148, over grids from one workgroup to one wave tile per wave,
+and over the Q6_K layouts with four rows per lane that the library refuses to
+launch (one of them, k_gemv<Q6_K, 2, 4, PLAIN, 4>, took a GPU memory fault
+once at 301 x 3584): every weight read, epilogue load, x pre-load and x
 staging access, LDS access and store stays inside its buffer.  A mistake
 planted in the model (an unclamped row or block index) is reported."""
 import itertools
