@@ -91,11 +91,19 @@ _SIGS = {
     "arc_exec148_materialize": [_P, _U32, _U32, _P, _P],
     "arc_exec148_validate": [_P, _P, _U32, _U32, C.POINTER(_U64), _P],
     "arc_exec148_validate_many": [C.POINTER(_P), C.POINTER(_P), _U32, _U32, _U32, C.POINTER(_U64), _P],
+    "arc_attention_workspace_bytes": [_U32, _U32],
+    "arc_attention_decode": [_P, _P, _P, _U32, _U32, _U32, _U32, _P, _P, _P],
+    "arc_prefill_gemm_workspace_bytes": [_U32, _U32],
+    "arc_prefill_gemm": [C.c_int, _P, _U32, _U32, _P, _U32, _P, _P, _P],
+    "arc_prefill_gateup": [_P, _P, _U32, _U32, _P, _U32, _P, _P, _P],
+    "arc_prefill_qkv": [_P, _P, _P, C.c_int, _U32, _U32, _U32, _P, _U32, _P, _P, _P],
 }
 _RESTYPE = {
     "arc_last_error": C.c_char_p,
     "arc_version": C.c_char_p,
     "arc_lmhead_workspace_bytes": C.c_size_t,
+    "arc_attention_workspace_bytes": C.c_size_t,
+    "arc_prefill_gemm_workspace_bytes": C.c_size_t,
 }
 MAX_LAYERS = 64
 T_TOKEN_EMBD, T_OUTPUT, T_OUTPUT_NORM, T_GLOBAL_COUNT = 0, 1, 2, 3
@@ -403,6 +411,45 @@ def lmhead_argmax_noalloc(qtype: int, w, rows: int, K: int, h, normw, eps: float
 def probe_read(buf, nbytes: int, out, grid: int = 2048, stream: Optional[Stream] = None) -> None:
     """Streaming-read probe (practical HBM read ceiling); `out` holds grid*256 uint32."""
     check(lib().arc_probe_read(_ptr(buf), nbytes, _ptr(out), grid, _sp(stream)))
+
+
+def attention_workspace_bytes(kv_heads: int, hpk: int) -> int:
+    n = int(lib().arc_attention_workspace_bytes(kv_heads, hpk))
+    if n == 0:
+        raise ArcError(2, f"no attention workspace size for {kv_heads} kv heads, {hpk} query heads each")
+    return n
+
+
+def attention_decode(q, kc, vc, kv_heads: int, hpk: int, max_ctx: int, T: int, out, workspace,
+                     stream: Optional[Stream] = None) -> None:
+    """The decode step's cached GQA over positions 0..T-1 (fp32 q/out, fp16 caches)."""
+    check(lib().arc_attention_decode(_ptr(q), _ptr(kc), _ptr(vc), kv_heads, hpk, max_ctx, T, _ptr(out),
+                                     _ptr(workspace), _sp(stream)))
+
+
+def prefill_gemm_workspace_bytes(N: int, K: int) -> int:
+    n = int(lib().arc_prefill_gemm_workspace_bytes(N, K))
+    if n == 0:
+        raise ArcError(1, f"no prompt-pass GEMM workspace size for {N} x {K}")
+    return n
+
+
+def prefill_gemm(qtype: int, w, N: int, K: int, x, M: int, y, workspace, stream: Optional[Stream] = None) -> None:
+    """The prompt pass's projection GEMM: y[M][N] (fp32) = x[M][K] (fp16) . w^T."""
+    check(lib().arc_prefill_gemm(qtype, _ptr(w), N, K, _ptr(x), M, _ptr(y), _ptr(workspace), _sp(stream)))
+
+
+def prefill_gateup(w_gate, w_up, N: int, K: int, x, M: int, s, workspace, stream: Optional[Stream] = None) -> None:
+    """The prompt pass's fused gate/up + SwiGLU: s[M][N] (fp16)."""
+    check(lib().arc_prefill_gateup(_ptr(w_gate), _ptr(w_up), N, K, _ptr(x), M, _ptr(s), _ptr(workspace),
+                                   _sp(stream)))
+
+
+def prefill_qkv(wq, wk, wv, v_qtype: int, H: int, kvd: int, K: int, x, M: int, y, workspace,
+                stream: Optional[Stream] = None) -> None:
+    """The prompt pass's q|k|v launch before bias and RoPE: y[M][H + 2 kvd] (fp32)."""
+    check(lib().arc_prefill_qkv(_ptr(wq), _ptr(wk), _ptr(wv), v_qtype, H, kvd, K, _ptr(x), M, _ptr(y),
+                                _ptr(workspace), _sp(stream)))
 
 
 def tune_force(bs: int, rpl: int) -> None:

@@ -143,7 +143,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
 #pragma unroll
         for (int i = 0; i < 8; ++i) qv[i] = qp[i];
     }
-    const uint32_t T = a.ctl->pos + 1;
+    const uint32_t T = min(a.ctl->pos + 1u, a.max_ctx);  // device memory: never past the cache
     const AttnSplit sp = attn_split(T);
     if (s >= sp.nsplit) return;  // whole workgroup: not part of this position's plan
     const uint32_t c0 = s * sp.cps, c1 = min(c0 + sp.cps, sp.nch);
@@ -174,8 +174,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
         uint32_t vc[kAttnTile];
 #pragma unroll
         for (int i = 0; i < 4; ++i) kc[i] = kr[i];
+        // rows at or past T (clamped or early loads: stale or never written)
+        // enter as zeros, so their weight 0 never multiplies an inf or NaN
 #pragma unroll
-        for (int j = 0; j < kAttnTile; ++j) vc[j] = vr[j];
+        for (int j = 0; j < kAttnTile; ++j) vc[j] = tw + j < T ? vr[j] : 0u;
         if (c + 1 < c1) load((c + 1) * kChunk, T - 1);
 
         f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -500,6 +502,7 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         p.cache = kc;
         p.rope = S->rope;
         p.ctl = S->ctl;
+        p.ctx_rows = S->max_ctx;
         p.y = S->q;
 
         // v projection + V store, in the same launch
@@ -511,12 +514,20 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         pv.kv_dim = KVD;
         pv.cache = vc;
         pv.ctl = S->ctl;
+        pv.ctx_rows = S->max_ctx;
         if (l == 0) {
+            // x is the decoded embedding row; workgroup 0 writes it to h.  The
+            // branch-free x pre-loads still read p.x: point it at a buffer
+            // this launch does not write (the values are discarded).
             p.flags |= F_EMBED;
             p.emb = M->emb;
+            p.emb_rows = d.vocab;
             p.h_out = S->h;
+            p.x = L.attn_norm;
             pv.flags |= F_EMBED;
             pv.emb = M->emb;
+            pv.emb_rows = d.vocab;
+            pv.x = L.attn_norm;
         }
         hipError_t e = L.v_type == kFmtQ4 ? launch_qkv<kFmtQ4>(p, pv, st) : launch_qkv<kFmtQ6P>(p, pv, st);
         if ((rc = chk(e, "q/k/v projection"))) return rc;
@@ -1107,5 +1118,87 @@ int arc_session_route_down(arc_session* s, uint32_t layer, const void* exec148)
 }
 
 uint32_t arc_session_prefill_kernels(const arc_session* s) { return s ? s->prefill_kernels : 0; }
+
+}  // extern "C"
+
+// --------------------------------------------- standalone decode attention
+namespace arc {
+
+// Zeroes the arrival counters and sets the control block's position for a
+// standalone attention launch (kernels, not memsets: callers may capture).
+__global__ void k_attn_setup(uint32_t* counters, uint32_t n, DecodeCtl* ctl, uint32_t pos)
+{
+    const uint32_t i = threadIdx.x;
+    if (i < n) counters[i] = 0u;
+    if (i == 0) *ctl = DecodeCtl{pos, 0u, 0u, 0u};
+}
+
+struct AttnWorkspace {
+    size_t po, pml, counters, ctl, bytes;
+};
+
+static AttnWorkspace attn_workspace(uint32_t kv_heads, uint32_t hpk)
+{
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    AttnWorkspace w{};
+    const size_t parts = size_t(kv_heads) * kMaxSplits * hpk;
+    w.po = 0;
+    w.pml = up(parts * kHeadDim * sizeof(float));
+    w.counters = w.pml + up(parts * 2 * sizeof(float));
+    w.ctl = w.counters + up(kv_heads * sizeof(uint32_t));
+    w.bytes = w.ctl + up(sizeof(DecodeCtl));
+    return w;
+}
+
+}  // namespace arc
+
+extern "C" {
+
+size_t arc_attention_workspace_bytes(uint32_t kv_heads, uint32_t hpk)
+{
+    if (kv_heads == 0 || kv_heads > uint32_t(kCounterLmHead - kCounterAttn) || hpk == 0 || hpk > uint32_t(kMaxHpk))
+        return 0;
+    return attn_workspace(kv_heads, hpk).bytes;
+}
+
+int arc_attention_decode(const float* q, const void* kc, const void* vc, uint32_t kv_heads, uint32_t hpk,
+                         uint32_t max_ctx, uint32_t T, float* out, void* workspace, arc_stream_t stream)
+{
+    if (!q || !kc || !vc || !out || !workspace) return set_error(ARC_ERR_INVALID_ARGUMENT, "null argument");
+    if (kv_heads == 0 || kv_heads > uint32_t(kCounterLmHead - kCounterAttn) || hpk == 0 || hpk > uint32_t(kMaxHpk))
+        return set_error(ARC_ERR_UNSUPPORTED, "attention supports 1..%d kv heads and 1..%d query heads per kv head",
+                         kCounterLmHead - kCounterAttn, kMaxHpk);
+    if (max_ctx == 0 || max_ctx > uint32_t(kMaxChunks * kChunk) || T == 0 || T > max_ctx)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "bad context: T %u, max_ctx %u (at most %d)", T, max_ctx,
+                         kMaxChunks * kChunk);
+    const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
+                         reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc);
+    if (al & 15u) return set_error(ARC_ERR_INVALID_ARGUMENT, "q, out, kc and vc must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+    const AttnWorkspace w = attn_workspace(kv_heads, hpk);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint32_t* counters = reinterpret_cast<uint32_t*>(ws + w.counters);
+    DecodeCtl* ctl = reinterpret_cast<DecodeCtl*>(ws + w.ctl);
+    hipLaunchKernelGGL(k_attn_setup, dim3(1), dim3(64), 0, st, counters, kv_heads, ctl, T - 1);
+    int rc = check_hip(hipGetLastError(), "attention setup");
+    if (rc) return rc;
+    AttnParams ap{};
+    ap.q = q;
+    ap.kc = static_cast<const _Float16*>(kc);
+    ap.vc = static_cast<const _Float16*>(vc);
+    ap.out = out;
+    ap.po = reinterpret_cast<float*>(ws + w.po);
+    ap.pml = reinterpret_cast<float*>(ws + w.pml);
+    ap.counter = counters;
+    ap.ctl = ctl;
+    ap.kv_heads = kv_heads;
+    ap.hpk = hpk;
+    ap.max_ctx = max_ctx;
+    ap.scale = 1.0f / std::sqrt(float(kHeadDim));
+    launch_attn(ap, dim3(kMaxSplits, kv_heads), st);
+    return check_hip(hipGetLastError(), "attention");
+}
 
 }  // extern "C"

@@ -96,6 +96,8 @@ struct GemvParams {
     uint32_t* counter;        // F_ARGNEXT: arrival counter (zero between launches)
     uint32_t* out_tokens;     // F_ARGNEXT: token of decode step ctl->step, if step < out_cap
     uint32_t out_cap;
+    uint32_t emb_rows;        // F_EMBED: rows of `emb` (a token id past them reads row 0)
+    uint32_t ctx_rows;        // QKROPE/VSTORE: rows of the cache and RoPE table (positions clamped below)
 };
 
 // ------------------------------------------------------------ block loads
@@ -663,9 +665,9 @@ __device__ __forceinline__ void st_group(float* p, const float4 (&q)[4])
 // thread's other groups first, then the first one, then the wave and
 // workgroup trees), and it is scaled and stored without a second read.
 template <int FMT, int NT>
-__device__ void stage_x_rms(float* lds, XPre<NT>& pre, const float* __restrict__ x, uint32_t nbl, float eps,
+__device__ void stage_x_rms(float* lds, XPre<NT>& pre, const float* x, uint32_t nbl, float eps,
                             const float* __restrict__ normw, float* red, const uint8_t* __restrict__ erow,
-                            float* __restrict__ raw_out)
+                            float* raw_out)
 {
     const uint32_t ng = nbl * 16u, gi0 = threadIdx.x;
     const bool have = gi0 < ng;
@@ -795,7 +797,7 @@ __device__ void argmax_finish(const GemvParams& p, uint32_t n)
     const ArgBest r = wg_argmax(bv, bi, nf);
     if (threadIdx.x == 0) {
         DecodeCtl* ctl = p.ctl;
-        const uint32_t tok = r.idx == 0xffffffffu ? 0u : r.idx;
+        const uint32_t tok = r.idx < p.rows ? r.idx : 0u;  // none (all non-finite): 0
         const uint32_t step = ctl->step;
         if (step < p.out_cap) p.out_tokens[step] = tok;
         ctl->token = tok;
@@ -925,6 +927,9 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
     // extra loads in flight recover).  The
     // first PF-1 loads are issued before the x staging.  Past the last item
     // the loads repeat it (a cache hit), keeping the sequence branch-free.
+    // (Refilling each buffer after it is consumed instead, with all PF
+    // first loads before the staging, measured slower: config-0 gate GEMV
+    // 12.3 -> 14.7 us, decode 610 -> 585 tokens/s at 512 positions.)
     Blk buf[PF][N];
     uint32_t li = 0, lj = 0, lnext = 1;  // next item to load; items issued so far
     auto advance = [&](uint32_t& i, uint32_t& j) {
@@ -944,7 +949,11 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
     // the embedding path exists only in the q/k/v epilogues (the first
     // layer's projections): its code costs the other GEMVs registers
     if constexpr (EPI == EPI_QKROPE || EPI == EPI_VSTORE)
-        if (rms && (p.flags & F_EMBED)) erow = p.emb + uint64_t(p.ctl->token) * p.nb * kQ4Bytes;
+        if (rms && (p.flags & F_EMBED)) {
+            // the control block is device memory: an id past the table reads row 0, never past it
+            const uint32_t tok = p.ctl->token;
+            erow = p.emb + uint64_t(tok < p.emb_rows ? tok : 0u) * p.nb * kQ4Bytes;
+        }
     XPre<NT> pre;
     x_pre<FMT, NT>(pre, p.x, kb, nbl, rms, p.normw);
 #pragma unroll
@@ -958,7 +967,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
     float ep_b[RPL], ep_r[RPL], ep_y[RPL];
     float2 ep_cs = {1.0f, 0.0f};
     uint32_t pos = 0;
-    if constexpr (EPI == EPI_QKROPE || EPI == EPI_VSTORE) pos = p.ctl->pos;
+    if constexpr (EPI == EPI_QKROPE || EPI == EPI_VSTORE) pos = min(p.ctl->pos, p.ctx_rows - 1u);
     auto load_ep = [&](uint32_t ti) {
         const uint32_t tile = min(gw + ti * stride, p.ntiles - 1);
 #pragma unroll

@@ -392,9 +392,10 @@ int arc_lmhead_argmax_noalloc(int qtype, const void* w, uint32_t rows, uint32_t 
     hipStream_t s = static_cast<hipStream_t>(stream);
     // size the grid first (host-side only): its workgroups must fit the scratch
     uint32_t gx = 0;
+    const bool dry = g_dry_run;
     g_dry_run = true;
     const hipError_t e = launch_gemv_epi(EPI_ARGMAX, qtype, c, p, 1, s, &gx);
-    g_dry_run = false;
+    g_dry_run = dry;
     if ((rc = check_hip(e, "lm-head sizing"))) return rc;
     if (gx > kNoAllocBest)
         return set_error(ARC_ERR_UNSUPPORTED, "LM-head launch needs %u workgroup results, the scratch holds %u", gx,

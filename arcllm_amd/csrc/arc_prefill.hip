@@ -222,17 +222,30 @@ __device__ __forceinline__ float mixc(uint32_t pair, bool hi, float A, float n)
     return __builtin_fmaf(static_cast<float>(hi ? h.y : h.x), A, n);
 }
 
+__device__ __forceinline__ float opaque_f(float v)
+{
+    asm("" : "+v"(v));
+    return v;
+}
+
 // Four weights from the four bytes of `codes` (each code < 2^10, in the low
 // bits of its byte or, for Q4_K high nibbles, times 16): bytes 0 and 2 are
 // the halves of codes & 0x00ff00ff, bytes 1 and 3 moved down by v_perm_b32.
+// Each weight is the element decode's fp32 value rounded to fp16.  Left to
+// itself the compiler fuses the fp32 FMA and the fp16 conversion into one
+// v_fma_mix{lo,hi}_f16, which rounds the exact d*sc*q - dmin*mn to fp16
+// directly; for Q4_K that value can need more bits than fp32 holds, and
+// where its fp32 rounding is an fp16 tie the two roundings differ by an fp16
+// ulp.  ROUND32 keeps the fp32 value (the reference's weight) in a register
+// first.  Q6_K's d*sc*(q-32) is exact in fp32, so the fused form is the same.
+template <bool ROUND32>
 __device__ __forceinline__ void mix4w(uint32_t codes, float A, float n, half8& o, int at)
 {
     const uint32_t ev = opaque(codes & 0x00ff00ffu);
     const uint32_t od = opaque(__builtin_amdgcn_perm(0u, codes, 0x0c030c01u));  // [b1, 0, b3, 0]
-    o[at + 0] = _Float16(mixc(ev, false, A, n));
-    o[at + 1] = _Float16(mixc(od, false, A, n));
-    o[at + 2] = _Float16(mixc(ev, true, A, n));
-    o[at + 3] = _Float16(mixc(od, true, A, n));
+    float w[4] = {mixc(ev, false, A, n), mixc(od, false, A, n), mixc(ev, true, A, n), mixc(od, true, A, n)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[at + i] = _Float16(ROUND32 ? opaque_f(w[i]) : w[i]);
 }
 
 // Step T of half HB: this lane's 8 weights as fp16, decoded in fp32 as one
@@ -252,8 +265,8 @@ __device__ __forceinline__ half8 dequant_step(const WDec<FMT>& w)
         constexpr int c = HB * 2 + (T >> 2), r = T & 3, j = 2 * c + (r >> 1);
         constexpr uint32_t mask = r < 2 ? 0x0f0f0f0fu : 0xf0f0f0f0u;
         const float A = w.f[j], n = w.g[j];
-        mix4w(w.qs[c][(r & 1) * 2] & mask, A, n, o, 0);
-        mix4w(w.qs[c][(r & 1) * 2 + 1] & mask, A, n, o, 4);
+        mix4w<true>(w.qs[c][(r & 1) * 2] & mask, A, n, o, 0);
+        mix4w<true>(w.qs[c][(r & 1) * 2 + 1] & mask, A, n, o, 4);
     } else {
         constexpr int q = T >> 1, u = T & 1;
         constexpr uint32_t lsh = (q >> 1) * 4u, hsh = q * 2u;
@@ -262,8 +275,8 @@ __device__ __forceinline__ half8 dequant_step(const WDec<FMT>& w)
         const uint32_t c0 = ((l[2 * u] >> lsh) & 0x0f0f0f0fu) | (((hh[2 * u] >> hsh) & 0x03030303u) << 4);
         const uint32_t c1 = ((l[2 * u + 1] >> lsh) & 0x0f0f0f0fu) | (((hh[2 * u + 1] >> hsh) & 0x03030303u) << 4);
         const float A = w.f[HB * 4 + q], n = w.n[HB * 4 + q];
-        mix4w(c0, A, n, o, 0);
-        mix4w(c1, A, n, o, 4);
+        mix4w<false>(c0, A, n, o, 0);
+        mix4w<false>(c1, A, n, o, 4);
     }
     return o;
 }
@@ -1243,3 +1256,186 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
 }
 
 }  // namespace arc
+
+// ------------------------------------ standalone prompt-pass projections
+namespace arc {
+namespace {
+
+struct PfWorkspace {
+    size_t x, part, bytes;
+};
+
+// X staging (256 rows of K fp16: the GEMM tiles read up to 256 rows) and the
+// split partials of the N x K projection's plan.
+PfWorkspace pf_workspace(uint32_t N, uint32_t K)
+{
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    uint32_t gx, sp, bps;
+    split_plan(N, K / kQK, gx, sp, bps);
+    PfWorkspace w{};
+    w.x = 0;
+    w.part = up(size_t(kPfMaxM) * K * sizeof(_Float16));
+    w.bytes = w.part + up(size_t(sp) * kPfMaxM * N * sizeof(float));
+    return w;
+}
+
+int pf_check(const void* w, uint32_t N, uint32_t K, const uint16_t* x, uint32_t M, const void* out, const void* ws)
+{
+    if (!w || !x || !out || !ws) return set_error(ARC_ERR_INVALID_ARGUMENT, "null argument");
+    if (N == 0 || K == 0 || K % kQK || M == 0 || M > uint32_t(kPfMaxM))
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "bad shape N=%u K=%u M=%u (K a multiple of 256, 1 <= M <= %d)", N, K,
+                         M, kPfMaxM);
+    if (N > uint32_t(kResCols) * 1024u) return set_error(ARC_ERR_UNSUPPORTED, "N must be <= %d", kResCols * 1024);
+    if (reinterpret_cast<uintptr_t>(w) & 15u) return set_error(ARC_ERR_INVALID_ARGUMENT, "weights not 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(ws) & 255u)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+    return ARC_OK;
+}
+
+// Copies the M given rows of X into the staging area and zeroes the rows the
+// tiles read past them (up to the 32-row block count of M).
+int pf_stage_x(uint8_t* ws, const PfWorkspace& w, const uint16_t* x, uint32_t M, uint32_t K, hipStream_t st)
+{
+    _Float16* xs = reinterpret_cast<_Float16*>(ws + w.x);
+    const size_t row = size_t(K) * sizeof(_Float16), rows = size_t(m_blocks(M)) * 32;
+    int rc = check_hip(hipMemcpyAsync(xs, x, M * row, hipMemcpyDeviceToDevice, st), "x staging");
+    if (rc) return rc;
+    if (rows > M) rc = check_hip(hipMemsetAsync(reinterpret_cast<uint8_t*>(xs) + M * row, 0, (rows - M) * row, st), "x pad");
+    return rc;
+}
+
+// y[m][c] = sum over the splits of part[s][m][c], in split order.
+int pf_reduce(const float* part, uint32_t splits, uint32_t M, uint32_t N, float* y, hipStream_t st)
+{
+    int rc = check_hip(hipMemsetAsync(y, 0, size_t(M) * N * sizeof(float), st), "y clear");
+    if (rc) return rc;
+    launch_res_norm<false>(M, st, part, splits, uint32_t(kPfMaxM), N, y, nullptr, 0.0f, nullptr, 0u);
+    return check_hip(hipGetLastError(), "split reduction");
+}
+
+}  // namespace
+}  // namespace arc
+
+using namespace arc;
+
+extern "C" {
+
+size_t arc_prefill_gemm_workspace_bytes(uint32_t N, uint32_t K)
+{
+    if (N == 0 || K == 0 || K % kQK) return 0;
+    return pf_workspace(N, K).bytes;
+}
+
+int arc_prefill_gemm(int qtype, const void* w, uint32_t N, uint32_t K, const uint16_t* x, uint32_t M, float* y,
+                     void* workspace, arc_stream_t stream)
+{
+    int rc = pf_check(w, N, K, x, M, y, workspace);
+    if (rc) return rc;
+    if (qtype != kFmtQ4 && qtype != kFmtQ6P)
+        return set_error(ARC_ERR_UNSUPPORTED, "the prompt-pass GEMM takes Q4_K or padded Q6_K (qtype %d)", qtype);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    const PfWorkspace pw = pf_workspace(N, K);
+    if ((rc = pf_stage_x(ws, pw, x, M, K, st))) return rc;
+    PfGemm g{};
+    g.M = M;
+    g.mpad = kPfMaxM;
+    g.x = reinterpret_cast<const _Float16*>(ws + pw.x);
+    g.ldx = K;
+    g.nb = K / kQK;
+    g.out = reinterpret_cast<float*>(ws + pw.part);
+    g.w0 = g.w1 = static_cast<const uint8_t*>(w);
+    g.row_bytes = uint64_t(g.nb) * (qtype == kFmtQ4 ? kQ4Bytes : kQ6PBytes);
+    g.ncol0 = N;
+    g.N = N;
+    g.ldo = N;
+    uint32_t gx, sp, bps;
+    split_plan(N, g.nb, gx, sp, bps);
+    g.bps = bps;
+    const uint32_t mb = m_blocks(M);
+    rc = check_hip(qtype == kFmtQ4 ? launch_gemm_mb<kFmtQ4, 1, false>(g, mb, gx, sp, st)
+                                   : launch_gemm_mb<kFmtQ6P, 1, false>(g, mb, gx, sp, st),
+                   "prompt-pass GEMM");
+    if (rc) return rc;
+    return pf_reduce(g.out, sp, M, N, y, st);
+}
+
+int arc_prefill_gateup(const void* w_gate, const void* w_up, uint32_t N, uint32_t K, const uint16_t* x, uint32_t M,
+                       uint16_t* s, void* workspace, arc_stream_t stream)
+{
+    int rc = pf_check(w_gate, N, K, x, M, s, workspace);
+    if (rc) return rc;
+    if (!w_up || (reinterpret_cast<uintptr_t>(w_up) & 15u))
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "up weights null or not 16-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    const PfWorkspace pw = pf_workspace(N, K);
+    if ((rc = pf_stage_x(ws, pw, x, M, K, st))) return rc;
+    PfGemm u{};
+    u.M = M;
+    u.mpad = kPfMaxM;
+    u.x = reinterpret_cast<const _Float16*>(ws + pw.x);
+    u.ldx = K;
+    u.nb = K / kQK;
+    u.w0 = static_cast<const uint8_t*>(w_gate);
+    u.w1 = static_cast<const uint8_t*>(w_up);
+    u.row_bytes = uint64_t(u.nb) * kQ4Bytes;
+    u.N = N;
+    u.ncol0 = N;
+    u.bps = u.nb;
+    u.s = reinterpret_cast<_Float16*>(s);
+    u.lds_out = N;
+    return check_hip(launch_gateup(u, m_blocks(M), (N + 127) / 128, st), "prompt-pass gate/up");
+}
+
+int arc_prefill_qkv(const void* wq, const void* wk, const void* wv, int v_qtype, uint32_t H, uint32_t kvd, uint32_t K,
+                    const uint16_t* x, uint32_t M, float* y, void* workspace, arc_stream_t stream)
+{
+    const uint32_t N = H + 2 * kvd;
+    int rc = pf_check(wq, N, K, x, M, y, workspace);
+    if (rc) return rc;
+    if (!wk || !wv || ((reinterpret_cast<uintptr_t>(wk) | reinterpret_cast<uintptr_t>(wv)) & 15u))
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "k or v weights null or not 16-byte aligned");
+    if (v_qtype != kFmtQ4 && v_qtype != kFmtQ6P)
+        return set_error(ARC_ERR_UNSUPPORTED, "v must be Q4_K or padded Q6_K (qtype %d)", v_qtype);
+    if (H == 0 || kvd == 0 || H % 128 || kvd % 128)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "H and kvd must be nonzero multiples of 128");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    const PfWorkspace pw = pf_workspace(N, K);
+    if ((rc = pf_stage_x(ws, pw, x, M, K, st))) return rc;
+    // as run_prefill: q|k one operand, v the other, partials [split][mpad][H | kvd | kvd]
+    PfGemm g{};
+    g.M = M;
+    g.mpad = kPfMaxM;
+    g.x = reinterpret_cast<const _Float16*>(ws + pw.x);
+    g.ldx = K;
+    g.nb = K / kQK;
+    g.out = reinterpret_cast<float*>(ws + pw.part);
+    g.w0 = static_cast<const uint8_t*>(wq);
+    g.w1 = static_cast<const uint8_t*>(wk);
+    g.row_bytes = uint64_t(g.nb) * kQ4Bytes;
+    g.ncol0 = H;
+    g.N = H + kvd;
+    g.ldo = N;
+    g.tiles = (g.N + 127) / 128;
+    PfGemm gv = g;
+    gv.w0 = gv.w1 = static_cast<const uint8_t*>(wv);
+    gv.row_bytes = uint64_t(g.nb) * (v_qtype == kFmtQ4 ? kQ4Bytes : kQ6PBytes);
+    gv.ncol0 = kvd;
+    gv.N = kvd;
+    gv.out = g.out + (H + kvd);
+    gv.tiles = (kvd + 127) / 128;
+    uint32_t gx, sp, bps;
+    split_plan(g.tiles * 128 + gv.tiles * 128, g.nb, gx, sp, bps);
+    g.bps = gv.bps = bps;
+    // the partial buffer is sized by the plan of N columns; the q|k|v plan's
+    // split count must fit it
+    uint32_t gx2, sp2, bps2;
+    split_plan(N, g.nb, gx2, sp2, bps2);
+    if (sp > sp2) return set_error(ARC_ERR_UNSUPPORTED, "internal: q/k/v split plan %u > workspace plan %u", sp, sp2);
+    if ((rc = check_hip(launch_qkv(g, gv, v_qtype, m_blocks(M), sp, st), "prompt-pass q/k/v"))) return rc;
+    return pf_reduce(g.out, sp, M, N, y, st);
+}
+
+}  // extern "C"

@@ -197,6 +197,50 @@ int arc_lmhead_argmax_noalloc(int qtype, const void *w, uint32_t rows, uint32_t 
                               const float *normw, float eps, float *logits, uint32_t *out,
                               arc_stream_t stream);
 
+/* Bytes of device workspace arc_attention_decode needs (split partials,
+ * arrival counters, control block); 0 for unsupported head counts. */
+size_t arc_attention_workspace_bytes(uint32_t kv_heads, uint32_t hpk);
+
+/* Cached GQA attention of one decode position, with the decode step's kernel
+ * and split plan: out[h*128 + d] = sum_t softmax_t(q_h . k_t / sqrt(128))
+ * v_t[d] over positions t < T, query head h reading kv head h / hpk.
+ * q, out: fp32 [kv_heads*hpk*128] (16-byte aligned); kc, vc: fp16
+ * [max_ctx][kv_heads*128] (16-byte aligned); 1 <= T <= max_ctx <= 32768;
+ * hpk 1..8.  workspace: arc_attention_workspace_bytes() bytes of device
+ * memory (256-byte aligned), owned by the caller and reset by the call.
+ * Replaces the decode attention dispatch of build_decode
+ * (src/arcllm_v1_runtime.cpp:371-421, shaders/p7_attention_kv_online.comp;
+ * semantics src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1177-1212). */
+int arc_attention_decode(const float *q, const void *kc, const void *vc, uint32_t kv_heads, uint32_t hpk,
+                         uint32_t max_ctx, uint32_t T, float *out, void *workspace, arc_stream_t stream);
+
+/* Bytes of device workspace the prompt-pass projection entry points need for
+ * an N x K weight (fp16 X staging of 256 rows and the split-K partials). */
+size_t arc_prefill_gemm_workspace_bytes(uint32_t N, uint32_t K);
+
+/* The prompt pass's projection GEMM, with its kernel and split-K plan:
+ * y[m][n] = sum_k x[m][k] w[n][k] for m < M <= 256, fp16 operands (each
+ * weight decoded in fp32 and rounded to fp16), fp32 accumulation, the split
+ * partials added in split order.  x: fp16 bits [M][K]; w: [N x K] Q4_K or
+ * ARC_Q6_K_PADDED; y: fp32 [M][N].  Replaces the p7c/p7g tiled GEMM
+ * dispatches of build_prefill (src/arcllm_v1_runtime.cpp:340-369). */
+int arc_prefill_gemm(int qtype, const void *w, uint32_t N, uint32_t K, const uint16_t *x, uint32_t M, float *y,
+                     void *workspace, arc_stream_t stream);
+
+/* The prompt pass's fused gate/up + SwiGLU GEMM (Q4_K gate and up):
+ * s[m][n] = fp16(silu(g) * u), g = x w_gate^T, u = x w_up^T, for m < M <= 256.
+ * x: fp16 bits [M][K]; s: fp16 bits [M][N].  workspace as for
+ * arc_prefill_gemm.  Replaces p7l (src/arcllm_v1_runtime.cpp:340-369). */
+int arc_prefill_gateup(const void *w_gate, const void *w_up, uint32_t N, uint32_t K, const uint16_t *x, uint32_t M,
+                       uint16_t *s, void *workspace, arc_stream_t stream);
+
+/* The prompt pass's q|k|v launch (Q4_K q and k, v Q4_K or ARC_Q6_K_PADDED):
+ * y[m][0..H) = x wq^T, y[m][H..H+kvd) = x wk^T, y[m][H+kvd..H+2kvd) = x wv^T
+ * (before bias and RoPE), fp32 [M][H + 2*kvd].  workspace:
+ * arc_prefill_gemm_workspace_bytes(H + 2*kvd, K). */
+int arc_prefill_qkv(const void *wq, const void *wk, const void *wv, int v_qtype, uint32_t H, uint32_t kvd, uint32_t K,
+                    const uint16_t *x, uint32_t M, float *y, void *workspace, arc_stream_t stream);
+
 /* Tuning hook: force the GEMV lane layout for later launches on this host
  * thread (bs = super-block quads per row: 1,2,4,8,16; rpl = rows per lane:
  * 1,2,4).  bs = 0 restores the automatic choice. */

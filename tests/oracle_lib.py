@@ -180,6 +180,17 @@ def splitk_r64(qtype: int, w: np.ndarray, rows: int, K: int, splits: int, x: np.
     return part.reshape(splits, rows)
 
 
+def attention_decode_f64(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, T: int, q_heads: int, kv_heads: int,
+                         dim: int = 128) -> np.ndarray:
+    """fp64 cached GQA over positions 0..T-1; kc/vc fp16 [ctx][kv_heads*dim]."""
+    q64 = np.ascontiguousarray(q, dtype=np.float64)
+    kb = np.ascontiguousarray(kc).view(np.uint16)
+    vb = np.ascontiguousarray(vc).view(np.uint16)
+    out = np.empty(q_heads * dim, dtype=np.float64)
+    oracle().orc_attention_decode_f64(_p(q64), _p(kb), _p(vb), T - 1, q_heads, kv_heads, dim, _p(out))
+    return out
+
+
 def rmsnorm_f64(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     x64 = np.ascontiguousarray(x, dtype=np.float64)
     y = np.empty_like(x64)
