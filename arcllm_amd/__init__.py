@@ -87,6 +87,7 @@ _SIGS = {
     "arc_synth_normal": [_U64, _U64, C.c_size_t, _F, _F, _P],
     "arc_tune_force": [C.c_int, C.c_int],
     "arc_tune_waves": [C.c_int],
+    "arc_tune_rowstream": [C.c_int],
     "arc_probe_read": [_P, C.c_size_t, _P, _U32, _P],
     "arc_exec148_materialize": [_P, _U32, _U32, _P, _P],
     "arc_exec148_validate": [_P, _P, _U32, _U32, C.POINTER(_U64), _P],
@@ -460,6 +461,12 @@ def tune_force(bs: int, rpl: int) -> None:
 def tune_waves(waves: int) -> None:
     """Force the waves per GEMV workgroup (4 or 8); 0 = automatic."""
     check(lib().arc_tune_waves(waves))
+
+
+def tune_rowstream(mode: int) -> None:
+    """Whole-row Q4_K GEMVs (K <= 3584): -1 automatic (default), 0 quad layout
+    only, 1 row-stream kernel."""
+    check(lib().arc_tune_rowstream(int(mode)))
 
 
 # ------------------------------------------------------- synthetic inputs

@@ -1166,6 +1166,12 @@ __global__ __launch_bounds__(W * kWave) void k_gemv(GemvParams p)
     gemv_body<FMT, BS, RPL, EPI, W>(p, blockIdx.x, gridDim.x);
 }
 
+}  // namespace arc
+
+#include "arc_gemv_rs.hpp"
+
+namespace arc {
+
 // --------------------------------------------------------------- launching
 struct Cfg {
     int bs, rpl, waves;  // quads per row, rows per lane, waves per workgroup (0 = default)
@@ -1231,6 +1237,61 @@ hipError_t launch_one(GemvParams p, uint32_t splits, hipStream_t s, uint32_t* gr
     if (g_dry_run) return hipSuccess;
     hipLaunchKernelGGL((k_gemv<FMT, BS, RPL, EPI, W>), dim3(uint32_t(gx), splits), dim3(W * kWave), lds, s, p);
     return hipGetLastError();
+}
+
+// Row-stream launches (arc_gemv_rs.hpp): 12-wave workgroups (one per CU at
+// 3 waves per SIMD: x is staged once per CU), the grid sized to the resident
+// workgroups and to one row tile per wave.
+constexpr int kRsWaves = 12;
+inline thread_local int g_rowstream = -1;  // -1 automatic, 0 quad layout only, 1 row-stream where eligible
+
+template <int NMAT, int RPL, int EPI, bool NORM, int W>
+hipError_t launch_rs(const GemvParams& p, hipStream_t s, uint32_t* grid_x)
+{
+    static int occ = 0;
+    if (!occ) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv_rs<NMAT, RPL, EPI, NORM, W>, W * kWave, 0) !=
+                hipSuccess ||
+            n < 1)
+            n = 1;
+        occ = n;
+    }
+    const int per_cu = g_wg_per_cu > 0 ? g_wg_per_cu : occ;
+    const uint64_t tiles = (p.rows + RPL - 1) / RPL;
+    const uint64_t want = (tiles + W - 1) / W;  // one tile per wave
+    uint64_t gx = uint64_t(per_cu) * cu_count();
+    if (gx > want) gx = want;
+    if (gx > 65536) gx = 65536;
+    if (grid_x) *grid_x = uint32_t(gx);
+    if (g_dry_run) return hipSuccess;
+    hipLaunchKernelGGL((k_gemv_rs<NMAT, RPL, EPI, NORM, W>), dim3(uint32_t(gx)), dim3(W * kWave), 0, s, p);
+    return hipGetLastError();
+}
+
+// Whether a launch takes the row-stream kernel: Q4_K, plain (without the
+// fused norm: no caller asks for it) or gate/up + SwiGLU, all of K (at most
+// 14 super-blocks) in this launch, no split-K, no embedding decode or
+// accumulation.  Automatic choice: plain GEMVs of 8192 rows or more, the
+// shapes it measured faster on (MI355X, 18944 x 3584: 10.9 vs 11.7 us;
+// 3584 x 3584: 5.6 vs 5.0 us, and the fused gate/up 20.0 vs 17.4 us).
+inline bool rs_eligible(int epi, const GemvParams& p, uint32_t splits)
+{
+    if (!g_rowstream || (epi != EPI_PLAIN && epi != EPI_SWIGLU)) return false;
+    if (splits != 1 || p.kb_off != 0 || p.panel != p.nb || p.split_bps != p.nb) return false;
+    if (p.nb < 1 || p.nb > uint32_t(kRsMaxBlocks)) return false;
+    if (p.flags & (F_EMBED | F_ACCUM | F_ARGNEXT)) return false;
+    if (epi == EPI_PLAIN && (p.flags & F_NORM)) return false;
+    if (g_rowstream < 0) return epi == EPI_PLAIN && p.rows >= 8192;
+    return true;
+}
+
+inline hipError_t launch_rs_epi(int epi, const GemvParams& p, hipStream_t s, uint32_t* gx)
+{
+    if (epi == EPI_SWIGLU)
+        return (p.flags & F_NORM) ? launch_rs<2, 1, EPI_SWIGLU, true, kRsWaves>(p, s, gx)
+                                  : launch_rs<2, 1, EPI_SWIGLU, false, kRsWaves>(p, s, gx);
+    return launch_rs<1, 1, EPI_PLAIN, false, kRsWaves>(p, s, gx);
 }
 
 // Forced configuration for tuning sweeps (bs = 0: automatic; waves = 0: automatic).
@@ -1320,6 +1381,8 @@ inline Cfg choose_cfg(int epi, uint32_t rows, uint32_t blocks, uint32_t splits)
 template <int EPI>
 hipError_t launch_gemv(int qtype, const Cfg& c, const GemvParams& p, uint32_t splits, hipStream_t s, uint32_t* gx)
 {
+    if constexpr (EPI == EPI_PLAIN || EPI == EPI_SWIGLU)
+        if (qtype == kFmtQ4 && !g_force.bs && rs_eligible(EPI, p, splits)) return launch_rs_epi(EPI, p, s, gx);
     if (qtype == kFmtQ4) return launch_cfg<kFmtQ4, EPI>(c, p, splits, s, gx);
     if (qtype == kFmtQ6P) return launch_cfg<kFmtQ6P, EPI>(c, p, splits, s, gx);
     if (qtype == kFmtE148) {

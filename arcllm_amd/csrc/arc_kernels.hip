@@ -228,6 +228,14 @@ int arc_tune_waves(int waves)
     return ARC_OK;
 }
 
+int arc_tune_rowstream(int mode)
+{
+    if (mode < -1 || mode > 1)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "row-stream mode must be -1 (automatic), 0 (off) or 1 (on)");
+    g_rowstream = mode;
+    return ARC_OK;
+}
+
 int arc_dequant(int qtype, const void* w, uint32_t rows, uint32_t K, float* out, arc_stream_t stream)
 {
     if (qtype == kFmtE148) return set_error(ARC_ERR_UNSUPPORTED, "arc_dequant takes Q4_K or Q6_K");

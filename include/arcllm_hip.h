@@ -248,6 +248,11 @@ int arc_tune_force(int bs, int rpl);
 /* Tuning hook: waves per GEMV workgroup (4 or 8) for later launches on this
  * host thread; 0 restores the automatic choice. */
 int arc_tune_waves(int waves);
+/* Tuning hook for whole-row Q4_K GEMVs (plain, gate/up; K <= 3584)
+ * launched or captured later on this host thread: -1 (default) automatic,
+ * 0 keeps every Q4_K launch on the quad layout, 1 takes the row-stream
+ * kernel. */
+int arc_tune_rowstream(int mode);
 
 /* Diagnostic: streaming read of `bytes` (16-byte aligned) with `grid`
  * workgroups of 256 lanes, 16 bytes per lane access, xor-folded into

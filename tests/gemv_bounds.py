@@ -268,3 +268,94 @@ def built_layouts(fmt):
     """The (bs, rpl) layouts launch_cfg instantiates (layout_built)."""
     lay = [(1, 1), (1, 2), (1, 4), (2, 1), (2, 2), (2, 4), (4, 1), (4, 2), (8, 1), (8, 2), (16, 1)]
     return [(b, r) for b, r in lay if not (fmt in (Q6, Q6P) and r == 4)]
+
+
+# ------------------------------------------------------------ row stream
+RS_MAX_BLOCKS, RS_OWNERS, RS_WAVES = 14, 56, 12
+RS_LDS_FLOATS = RS_MAX_BLOCKS * KQK // 64 * 68
+
+
+def rs_lds_index(e):
+    """arc_gemv_rs.hpp rs_lds_index: 4 pad floats after every 64."""
+    return e + 4 * (e >> 6)
+
+
+def simulate_rs(rows: int, K: int, epi: int, norm: bool, gx: int | None = None, ring: int = 3,
+                mistake: str | None = None) -> Report:
+    """Bounds model of gemv_rs_body (arc_gemv_rs.hpp) and launch_rs: every
+    thread's x / norm-weight float4 loads (indices clamped), the LDS stores
+    of the staging and each lane's reads of its 64 values, the weight chunk
+    and header loads of the ring (clamped tile, row and block, and the loads
+    past the last tile), the epilogue operand loads, the bpermute source
+    lane, the block-sum slots and the output stores.  `mistake` = "block"
+    drops the owner lanes' block clamp, "row" the tile and row clamps."""
+    rep = Report()
+    nb = K // KQK
+    assert 1 <= nb <= RS_MAX_BLOCKS, "launch_rs takes rows of 1 .. 14 super-blocks"
+    W = RS_WAVES
+    NT = W * WAVE
+    XQ = -(-(RS_MAX_BLOCKS * KQK // 4) // NT)
+    nq = nb * KQK // 4
+    row_bytes = nb * 144
+    nmat = 2 if epi == SWIGLU else 1
+    ntiles = rows
+    want = -(-ntiles // W)
+    if gx is None:
+        gx = min(want, 256)
+    assert 1 <= gx <= want
+    t = np.arange(NT)
+    lane, wave = t & 63, t >> 6
+
+    for i in range(XQ):
+        q = np.minimum(t + i * NT, nq - 1)
+        rep.check("x float4 load", 4 * q, 4 * q + 4, 0, K)
+        if norm:
+            rep.check("norm weight float4 load", 4 * q, 4 * q + 4, 0, K)
+        st = t + i * NT
+        st = st[st < nq]
+        li = rs_lds_index(4 * st)
+        rep.check("LDS x store", li, li + 4, 0, RS_LDS_FLOATS)
+    rep.check("block-sum slot", wave, wave + 1, 0, W)
+
+    header = lane >= RS_OWNERS
+    k = np.where(header, 0, lane >> 2)
+    g = lane & 3
+    owner = ~header & (k < nb)
+    hk = lane - RS_OWNERS
+    kc = k if mistake == "block" else np.minimum(k, nb - 1)
+    oa = np.where(header, np.minimum(hk, nb - 1) * 144, kc * 144 + 16 + 32 * g)
+    ob = np.where(header, np.minimum(hk + 8, nb - 1) * 144, oa + 16)
+    src = RS_OWNERS + (k & 7)
+    rep.check("bpermute source lane", src, src + 1, 0, WAVE)
+    xe = rs_lds_index(np.minimum(k, nb - 1) * KQK + 64 * g)
+    rep.check("LDS x read", xe, xe + 64, 0, RS_LDS_FLOATS)
+
+    clamp_tile = (lambda v: v) if mistake == "row" else (lambda v: min(v, ntiles - 1))
+    stride = gx * W
+    for bx in range(gx):
+        for wv in range(W):
+            gw = bx * W + wv
+            my = (ntiles - gw + stride - 1) // stride if gw < ntiles else 0
+            lane_sel = wave == wv
+
+            def load(ti):
+                tile = clamp_tile(gw + ti * stride)
+                row = tile if mistake == "row" else min(tile, rows - 1)
+                for m in range(nmat):
+                    for o in (oa, ob):
+                        off = row * row_bytes + o[lane_sel]
+                        rep.check(f"weight load (w{m})", off, off + 16, 0, rows * row_bytes)
+                if epi == PLAIN:
+                    rep.check("epilogue operand load", np.array([row]), np.array([row + 1]), 0, rows)
+
+            # the ring: items 0 .. ring-2 first, then item t + ring - 1 before
+            # consuming item t, for t < (my // ring) * ring
+            for i in range(ring - 1):
+                load(i)
+            full = (my // ring) * ring
+            for tt in range(full):
+                load(tt + ring - 1)
+            for ti in range(my):
+                row = gw + ti * stride
+                rep.check("output store", np.array([row]), np.array([row + 1]), 0, rows)
+    return rep

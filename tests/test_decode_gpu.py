@@ -117,6 +117,31 @@ def test_tiny_model_first_step_logits_and_eager_replay():
     assert np.array_equal(np.concatenate([t1, t2]), ta)
 
 
+def test_tiny_model_row_stream_gemvs_forced():
+    """The decode step with the row-stream kernel forced on: the o projection
+    and Q4_K down (residual epilogue), the fused gate/up with the ffn norm.
+    First-step logits against the fp64 oracle, then 64 greedy steps."""
+    d = tiny_dims(layers=3)
+    T = arc.synth_model_tensors(d, SEED)
+    model = arc.Model(d, T)
+    arc.tune_rowstream(1)
+    try:
+        s1 = arc.Session(model, 128)
+        s1.fill_kv(40, 5)
+        tok, _ = s1.decode(9, 40, 1, logits=True)
+        lg = s1.logits()
+        sess, gpu, nf, ref, second, margins, scale = run_pair(d, T, model, 256, 100, 17, 64, 11)
+    finally:
+        arc.tune_rowstream(-1)
+    o = orc.DecodeOracle(d, T, 128)
+    o.fill_kv(40, 5, arc.synth_normal)
+    ref1 = o.step(9, 40)
+    e2e_check(lg, ref1, "tiny model, row-stream forced, ctx 40")
+    assert int(tok[0]) == int(np.argmax(ref1))
+    assert nf == 0
+    assert assert_tokens_match(gpu, ref, second, margins, scale) >= 48
+
+
 def test_seven_query_heads_per_kv_head_long_context():
     """The 7B model's GQA grouping (7 query heads per kv head) on a small
     model, at a context long enough for several attention splits per kv head

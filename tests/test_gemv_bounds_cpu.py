@@ -89,3 +89,39 @@ def test_planted_index_mistake_is_reported(mistake):
         for gx, r in run(c, mistake):
             found |= bool(r.violations)
     assert found
+
+
+RS_SHAPES = [(1, 256), (4, 256), (37, 512), (301, 3584), (1000, 3584), (13, 2560)]
+
+
+def rs_cases():
+    for rows, K in RS_SHAPES:
+        want = -(-rows // gb.RS_WAVES)
+        for gx in sorted({1, min(want, 3), want, min(want, 256)}):
+            for ring in (2, 3, 4):
+                yield rows, K, gb.PLAIN, False, gx, ring
+                yield rows, K, gb.SWIGLU, True, gx, ring
+                yield rows, K, gb.SWIGLU, False, gx, ring
+
+
+def test_row_stream_launches_stay_in_bounds():
+    """The row-stream Q4_K kernel (plain and gate/up + SwiGLU, with and
+    without the fused norm) for 1 to 14 super-blocks per row, ragged row
+    counts, ring depths 2 to 4 and grids from one workgroup to one row per
+    wave."""
+    bad = []
+    n = 0
+    for rows, K, epi, norm, gx, ring in rs_cases():
+        r = gb.simulate_rs(rows, K, epi, norm, gx, ring)
+        n += r.checked
+        if r.violations:
+            bad.append(((rows, K, epi, norm, gx, ring), r.violations[:3]))
+    assert n > 0
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("mistake", ["block", "row"])
+def test_row_stream_planted_mistake_is_reported(mistake):
+    # 2 super-blocks: owner lanes of blocks 2 .. 13 sit past the row
+    r = gb.simulate_rs(37, 512, gb.PLAIN, False, 2, mistake=mistake)
+    assert r.violations

@@ -230,6 +230,50 @@ def test_gateup_swiglu(rows, K):
 
 
 @pytest.mark.parametrize(
+    "rows,K,bias",
+    [(4, 256, False), (37, 512, True), (301, 2560, True), (1000, 3584, False), (3584, 3584, True), (18944, 3584, False)],
+)
+def test_rowstream_gemv_vs_fp64(rows, K, bias):
+    """The row-stream Q4_K kernel forced on for every shape it takes (the
+    automatic choice gives it plain GEMVs of 8192 rows or more)."""
+    w = packed(arc.Q4_K, rows, K, 40)
+    x = arc.synth_normal(SEED, 41, K)
+    b = arc.synth_normal(SEED, 42, rows) if bias else None
+    y = arc.DeviceBuffer(rows * 4)
+    arc.tune_rowstream(1)
+    try:
+        arc.gemv(arc.Q4_K, dev(w), rows, K, dev(x), y, bias=None if b is None else dev(b))
+    finally:
+        arc.tune_rowstream(-1)
+    err = orc.rel_err(y.download(np.float32), orc.gemv_r64(arc.Q4_K, w, rows, K, x, b))
+    print(f"rel_err={err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("rows,K", [(64, 512), (1000, 3584), (18944, 3584)])
+def test_rowstream_gateup_swiglu(rows, K):
+    wg = packed(arc.Q4_K, rows, K, 43)
+    wu = packed(arc.Q4_K, rows, K, 44)
+    x = arc.synth_normal(SEED, 45, K)
+    s = arc.DeviceBuffer(rows * 4)
+    arc.tune_rowstream(1)
+    try:
+        arc.gateup_swiglu(arc.Q4_K, dev(wg), dev(wu), rows, K, dev(x), s)
+    finally:
+        arc.tune_rowstream(-1)
+    g = orc.gemv_r64(arc.Q4_K, wg, rows, K, x)
+    u = orc.gemv_r64(arc.Q4_K, wu, rows, K, x)
+    err = orc.rel_err(s.download(np.float32), orc.swiglu_f64(g, u))
+    print(f"rel_err={err:.3e}")
+    assert err <= TOL
+
+
+def test_rowstream_mode_rejects_bad_values():
+    with pytest.raises(arc.ArcError):
+        arc.tune_rowstream(2)
+
+
+@pytest.mark.parametrize(
     "qtype,rows,K,splits",
     [(arc.Q6_K, 3584, 18944, 74), (arc.Q6_K, 100, 2560, 3), (arc.Q4_K, 512, 2560, 5), (arc.Q4_K, 3584, 18944, 74),
      (arc.Q6_K, 33, 2304, 9), (arc.Q4_K, 70, 38400, 150)],
