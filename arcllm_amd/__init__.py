@@ -88,6 +88,7 @@ _SIGS = {
     "arc_tune_force": [C.c_int, C.c_int],
     "arc_tune_waves": [C.c_int],
     "arc_tune_rowstream": [C.c_int],
+    "arc_tune_attention": [C.c_int, C.c_int],
     "arc_probe_read": [_P, C.c_size_t, _P, _U32, _P],
     "arc_exec148_materialize": [_P, _U32, _U32, _P, _P],
     "arc_exec148_validate": [_P, _P, _U32, _U32, C.POINTER(_U64), _P],
@@ -461,6 +462,12 @@ def tune_force(bs: int, rpl: int) -> None:
 def tune_waves(waves: int) -> None:
     """Force the waves per GEMV workgroup (4 or 8); 0 = automatic."""
     check(lib().arc_tune_waves(waves))
+
+
+def tune_attention(waves: int = 0, min_chunks_per_split: int = 0) -> None:
+    """Decode attention launch shape: waves per workgroup (4 or 8) and the
+    least chunks of 16 * waves positions per split; 0 = automatic."""
+    check(lib().arc_tune_attention(int(waves), int(min_chunks_per_split)))
 
 
 def tune_rowstream(mode: int) -> None:

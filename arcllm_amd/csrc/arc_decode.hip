@@ -39,35 +39,37 @@ struct AttnParams {
     const DecodeCtl* ctl;
     uint32_t kv_heads, hpk;
     uint32_t max_ctx;         // cache rows per layer (loads are clamped to it)
+    uint32_t min_cps;         // chunks per split at least (>= 1)
     float scale;
 };
 
 // Split plan of one decode position over T cached positions: chunks of
-// kChunk positions, each split (workgroup) taking a run of cps consecutive
-// chunks in turn, at most kMaxSplits splits per kv head (one chunk per split
-// up to 2048 positions).  Measured on the 7B shape: one chunk per split with
-// the merge beats two chunks per split with half the merging (571 vs 551
-// tokens/s at 512 positions).
+// `chunk` positions (16 per wave of the workgroup), each split (workgroup)
+// taking a run of cps consecutive chunks in turn, at least min_cps and at
+// most kMaxSplits splits per kv head.
 struct AttnSplit {
     uint32_t nch, cps, nsplit;
 };
-__device__ __host__ inline AttnSplit attn_split(uint32_t T)
+__device__ __host__ inline AttnSplit attn_split(uint32_t T, uint32_t chunk, uint32_t min_cps)
 {
-    const uint32_t nch = (T + kChunk - 1) / kChunk;
-    const uint32_t cps = (nch + kMaxSplits - 1) / kMaxSplits;
+    const uint32_t nch = (T + chunk - 1) / chunk;
+    uint32_t cps = (nch + kMaxSplits - 1) / kMaxSplits;
+    if (cps < min_cps) cps = min_cps;
     return AttnSplit{nch, cps, (nch + cps - 1) / cps};
 }
 
-// k_attn: 4 waves per workgroup; wave w takes positions 16w .. 16w+15 of
-// every chunk of kChunk positions, with its own running softmax state.
-constexpr int kAttnWaves = 4;
-constexpr int kAttnThreads = kAttnWaves * kWave;
+// k_attn: W waves per workgroup; wave w takes positions 16w .. 16w+15 of
+// every chunk of 16 W positions, with its own running softmax state.
 constexpr int kAttnTile = 16;  // positions per wave and chunk (the MFMA rows)
-static_assert(kChunk == kAttnWaves * kAttnTile, "one 16-position MFMA tile per wave");
+static_assert(kChunk == 4 * kAttnTile, "the session's chunk: 4 waves of 16 positions");
 static_assert(kHeadDim == 2 * kWave, "V sum: one dim pair per lane");
 static_assert(kMaxSplits <= kWave, "the merge takes one split per lane");
 constexpr int kAttnMergeBatch = 16;  // split outputs loaded per batch in the merge
-constexpr uint32_t kAttnEarlySplits = 8;  // splits that load before reading the position
+// Splits that load their first chunk before reading the position: with 4
+// waves, splits 0..7 take part in every plan above 448 positions; with 8,
+// splits 0..3 (plans above 384 positions).
+template <int W>
+constexpr uint32_t attn_early_splits() { return W == 4 ? 8u : 4u; }
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -102,14 +104,16 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 // workgroup arrives last.
 // Semantics: src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1177-1212,
 // shaders/p7_attention_kv_online.comp (kv head = q head / (q_heads/kv_heads)).
-template <int HPK>
-__global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
+template <int HPK, int W>
+__global__ __launch_bounds__(W * kWave) void k_attn(AttnParams a)
 {
-    __shared__ __align__(16) float pw[kAttnWaves][kAttnTile][8];  // per wave: weights [position][head]
-    __shared__ __align__(16) float fow[kAttnWaves][8];            // per wave: rescale per head
-    __shared__ float mw[kAttnWaves][8], lw[kAttnWaves][8];         // split end: wave (max, sum) per head
-    __shared__ __align__(16) float ow[kAttnWaves][HPK][kHeadDim];  // split end: wave o per head
-    __shared__ float fw[kMaxSplits][HPK];                          // merge: split weights
+    constexpr int kC = W * kAttnTile;  // positions per chunk
+    static_assert(W == 4 || W == 8, "4 or 8 waves per workgroup");
+    __shared__ __align__(16) float pw[W][kAttnTile][8];  // per wave: weights [position][head]
+    __shared__ __align__(16) float fow[W][8];            // per wave: rescale per head
+    __shared__ float mw[W][8], lw[W][8];                 // split end: wave (max, sum) per head
+    __shared__ __align__(16) float ow[W][HPK][kHeadDim];  // split end: rescaled wave o per head
+    __shared__ float fw[kMaxSplits][HPK];                // merge: split weights
     __shared__ uint32_t flag;
 
     const uint32_t s = blockIdx.x, g = blockIdx.y;
@@ -135,8 +139,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
     // their first chunk's loads before the position is known.  The others
     // read the position first, so the splits a short context leaves idle
     // read nothing.
-    const bool early = s < kAttnEarlySplits;
-    if (early) load(s * kChunk, a.max_ctx - 1);  // chunk s: the first chunk of split s when cps = 1
+    const bool early = s < attn_early_splits<W>();
+    if (early) load(s * kC, a.max_ctx - 1);  // chunk s: the first chunk of split s when cps = 1
     float4 qv[8];
     {
         const float4* qp = reinterpret_cast<const float4*>(a.q + (uint64_t(g) * HPK + min(r16, HPK - 1)) * kHeadDim + 32 * grp);
@@ -144,10 +148,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
         for (int i = 0; i < 8; ++i) qv[i] = qp[i];
     }
     const uint32_t T = min(a.ctl->pos + 1u, a.max_ctx);  // device memory: never past the cache
-    const AttnSplit sp = attn_split(T);
+    const AttnSplit sp = attn_split(T, kC, a.min_cps);
     if (s >= sp.nsplit) return;  // whole workgroup: not part of this position's plan
     const uint32_t c0 = s * sp.cps, c1 = min(c0 + sp.cps, sp.nch);
-    if (sp.cps != 1 || !early) load(c0 * kChunk, T - 1);
+    if (sp.cps != 1 || !early) load(c0 * kC, T - 1);
 
     half8_t qh[4], ql[4];  // B operand: head r16 (zero past HPK), dims 32grp + 8ks .. +7
 #pragma unroll
@@ -169,7 +173,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
     float M = -INFINITY, Ls = 0.0f;  // head r16: running max, this lane's share of the running sum
     float (*pwr)[8] = pw[w];
     for (uint32_t c = c0; c < c1; ++c) {
-        const uint32_t tw = c * kChunk + kAttnTile * w;
+        const uint32_t tw = c * kC + kAttnTile * w;
         uint4 kc[4];
         uint32_t vc[kAttnTile];
 #pragma unroll
@@ -178,7 +182,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
         // enter as zeros, so their weight 0 never multiplies an inf or NaN
 #pragma unroll
         for (int j = 0; j < kAttnTile; ++j) vc[j] = tw + j < T ? vr[j] : 0u;
-        if (c + 1 < c1) load((c + 1) * kChunk, T - 1);
+        if (c + 1 < c1) load((c + 1) * kC, T - 1);
 
         f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -229,12 +233,23 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
         }
     }
 
-    // the waves' states into LDS, combined per (head, dim quad) in wave order
+    // the waves' states combined in LDS: the split's max per head, each wave's
+    // o rescaled by e^(m_w - M), then per (head, dim quad) the waves in order
     Ls = xor_sum<16>(Ls);
     Ls = xor_sum<32>(Ls);
     if (grp == 0 && r16 < HPK) {
         mw[w][r16] = M;
         lw[w][r16] = Ls;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < HPK; ++h) {
+        float Mh = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < W; ++v) Mh = fmaxf(Mh, mw[v][h]);  // finite: the split holds a position < T
+        const float f = expf(mw[w][h] - Mh);                   // a wave without positions < T: e^-inf = 0
+        o0[h] *= f;
+        o1[h] *= f;
     }
 #pragma unroll
     for (int h = 0; h < HPK; ++h) reinterpret_cast<float2*>(ow[w][h])[lane] = make_float2(o0[h], o1[h]);
@@ -246,16 +261,16 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
     float4 osp = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     {
 #pragma unroll
-        for (int v = 0; v < kAttnWaves; ++v) Msp = fmaxf(Msp, mw[v][hh]);  // finite: the split holds a position < T
+        for (int v = 0; v < W; ++v) Msp = fmaxf(Msp, mw[v][hh]);
 #pragma unroll
-        for (int v = 0; v < kAttnWaves; ++v) {
-            const float f = expf(mw[v][hh] - Msp);  // a wave without positions < T: e^-inf = 0
+        for (int v = 0; v < W; ++v) Lsp = __builtin_fmaf(lw[v][hh], expf(mw[v][hh] - Msp), Lsp);
+#pragma unroll
+        for (int v = 0; v < W; ++v) {
             const float4 ov = reinterpret_cast<const float4*>(ow[v][hh])[dq4];
-            Lsp = __builtin_fmaf(lw[v][hh], f, Lsp);
-            osp.x = __builtin_fmaf(ov.x, f, osp.x);
-            osp.y = __builtin_fmaf(ov.y, f, osp.y);
-            osp.z = __builtin_fmaf(ov.z, f, osp.z);
-            osp.w = __builtin_fmaf(ov.w, f, osp.w);
+            osp.x += ov.x;
+            osp.y += ov.y;
+            osp.z += ov.z;
+            osp.w += ov.w;
         }
     }
 
@@ -283,16 +298,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
     if (!arrive_last(a.counter + g, sp.nsplit, &flag)) return;
 
     // merge (last workgroup of kv head g).  Wave w, lane = split: the split
-    // weights w_s = e^(m_s - M) / L of heads w, w + 4 (M and L by wave
+    // weights w_s = e^(m_s - M) / L of heads w, w + W (M and L by wave
     // reductions) into LDS; then thread -> (head hh, dims 4dq4 .. +3) sums
     // the splits' o weighted, in split order, loads in batches of kB (the
     // first batch is issued right after the (m, l) loads).
     const bool in = uint32_t(lane) < sp.nsplit;
     const uint32_t ss = min(uint32_t(lane), sp.nsplit - 1);
-    float2 ml[2];
+    float2 ml[2];  // at most 2 heads per wave (W >= 4)
+    constexpr int kMH = (kMaxHpk + W - 1) / W;  // heads per wave in the merge
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const uint32_t h = min(uint32_t(w + kAttnWaves * k), uint32_t(HPK - 1));
+    for (int k = 0; k < kMH; ++k) {
+        const uint32_t h = min(uint32_t(w + W * k), uint32_t(HPK - 1));
         ml[k] = ld_agent2(a.pml + ((base + ss) * HPK + h) * 2);
     }
     const float* src = a.po + (base * HPK + hh) * kHeadDim + 4 * dq4;
@@ -308,8 +324,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
     };
     if (owner) fetch(0);
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int h = w + kAttnWaves * k;
+    for (int k = 0; k < kMH; ++k) {
+        const int h = w + W * k;
         if (h < HPK) {
             const float m = in ? ml[k].x : -INFINITY;
             const float Mx = wave_max(m);
@@ -337,31 +353,54 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams a)
     }
 }
 
-template <int HPK>
-static void launch_attn_hpk(const AttnParams& ap, dim3 grid, hipStream_t st)
+// Attention launch shape (tuning): waves per workgroup and the least chunks
+// per split.  Measured on MI355X (7B shape, 28 q / 4 kv heads): 4 waves,
+// one chunk per split 10.2 / 13.2 / 17.9 us at 512 / 2048 / 4096 positions,
+// 8 waves 11.3 / 12.4 / 14.9 us, 16 waves 17.7 / 18.2 / 18.8 us, two or
+// more chunks per split slower at every length; decode tokens/s with 8
+// waves -1.8% at 512 positions, +1.1% at 2048, equal at 4096.  Automatic:
+// 4 waves, one chunk per split.
+inline thread_local int g_attn_waves = 0;    // 0: automatic
+inline thread_local int g_attn_min_cps = 0;  // 0: automatic
+
+template <int HPK, int W>
+static void launch_attn_hpk(const AttnParams& ap, uint32_t kv_heads, hipStream_t st)
 {
     if (g_dry_run) return;
-    hipLaunchKernelGGL(k_attn<HPK>, grid, dim3(kAttnThreads), 0, st, ap);
+    hipLaunchKernelGGL((k_attn<HPK, W>), dim3(kMaxSplits, kv_heads), dim3(W * kWave), 0, st, ap);
 }
 
-// hpk is 1..kMaxHpk (checked with the model dims)
-static void launch_attn(const AttnParams& ap, dim3 grid, hipStream_t st)
+template <int W>
+static void launch_attn_w(const AttnParams& ap, uint32_t kv_heads, hipStream_t st)
 {
     switch (ap.hpk) {
-    case 1: launch_attn_hpk<1>(ap, grid, st); break;
-    case 2: launch_attn_hpk<2>(ap, grid, st); break;
-    case 3: launch_attn_hpk<3>(ap, grid, st); break;
-    case 4: launch_attn_hpk<4>(ap, grid, st); break;
-    case 5: launch_attn_hpk<5>(ap, grid, st); break;
-    case 6: launch_attn_hpk<6>(ap, grid, st); break;
-    case 7: launch_attn_hpk<7>(ap, grid, st); break;
-    default: launch_attn_hpk<8>(ap, grid, st); break;
+    case 1: launch_attn_hpk<1, W>(ap, kv_heads, st); break;
+    case 2: launch_attn_hpk<2, W>(ap, kv_heads, st); break;
+    case 3: launch_attn_hpk<3, W>(ap, kv_heads, st); break;
+    case 4: launch_attn_hpk<4, W>(ap, kv_heads, st); break;
+    case 5: launch_attn_hpk<5, W>(ap, kv_heads, st); break;
+    case 6: launch_attn_hpk<6, W>(ap, kv_heads, st); break;
+    case 7: launch_attn_hpk<7, W>(ap, kv_heads, st); break;
+    default: launch_attn_hpk<8, W>(ap, kv_heads, st); break;
     }
 }
+
+// Sets ap.min_cps and launches (grid: kMaxSplits x kv heads; workgroups past
+// the position's plan return at once).
+static void launch_attn(AttnParams ap, uint32_t kv_heads, hipStream_t st)
+{
+    const int waves = g_attn_waves ? g_attn_waves : 4;
+    ap.min_cps = g_attn_min_cps > 0 ? uint32_t(g_attn_min_cps) : 1u;
+    if (waves == 8)
+        launch_attn_w<8>(ap, kv_heads, st);
+    else
+        launch_attn_w<4>(ap, kv_heads, st);
+}
+
 static_assert(kMaxHpk == 8, "launch_attn instantiates 1..8");
 static_assert(kMaxHpk <= 16, "query heads of a kv head fit the 16 MFMA columns");
-static_assert(kMaxHpk * (kHeadDim / 4) <= kAttnThreads && kMaxHpk <= 2 * kAttnWaves,
-              "merge: one thread per (head, dim quad); two heads per wave for the split weights");
+static_assert(kMaxHpk * (kHeadDim / 4) <= 4 * kWave && kMaxHpk <= 2 * 4,
+              "merge (4 waves): one thread per (head, dim quad); at most two heads per wave for the split weights");
 
 }  // namespace arc
 
@@ -546,7 +585,7 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         ap.hpk = d.q_heads / d.kv_heads;
         ap.max_ctx = S->max_ctx;
         ap.scale = 1.0f / std::sqrt(float(kHeadDim));
-        launch_attn(ap, dim3(kMaxSplits, d.kv_heads), st);
+        launch_attn(ap, d.kv_heads, st);
         if ((rc = chk(hipGetLastError(), "attention"))) return rc;
 
         // o projection + residual: h1 = h + Wo attn
@@ -588,6 +627,17 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
 using namespace arc;
 
 extern "C" {
+
+int arc_tune_attention(int waves, int min_chunks_per_split)
+{
+    if (waves != 0 && waves != 4 && waves != 8)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "attention waves per workgroup must be 0 (automatic), 4 or 8");
+    if (min_chunks_per_split < 0 || min_chunks_per_split > kMaxChunks)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "chunks per split must be 0 (automatic) .. %d", kMaxChunks);
+    g_attn_waves = waves;
+    g_attn_min_cps = min_chunks_per_split;
+    return ARC_OK;
+}
 
 int arc_model_dims_qwen25_7b(arc_model_dims* d)
 {
@@ -1197,7 +1247,7 @@ int arc_attention_decode(const float* q, const void* kc, const void* vc, uint32_
     ap.hpk = hpk;
     ap.max_ctx = max_ctx;
     ap.scale = 1.0f / std::sqrt(float(kHeadDim));
-    launch_attn(ap, dim3(kMaxSplits, kv_heads), st);
+    launch_attn(ap, kv_heads, st);
     return check_hip(hipGetLastError(), "attention");
 }
 

@@ -253,6 +253,10 @@ int arc_tune_waves(int waves);
  * 0 keeps every Q4_K launch on the quad layout, 1 takes the row-stream
  * kernel. */
 int arc_tune_rowstream(int mode);
+/* Tuning hook for decode attention launched or captured later on this host
+ * thread: waves per workgroup (4 or 8; a chunk is 16 positions per wave)
+ * and the least chunks one split (workgroup) covers; 0 = automatic. */
+int arc_tune_attention(int waves, int min_chunks_per_split);
 
 /* Diagnostic: streaming read of `bytes` (16-byte aligned) with `grid`
  * workgroups of 256 lanes, 16 bytes per lane access, xor-folded into

@@ -67,6 +67,31 @@ def test_attention_decode_vs_fp64(kv_cache, T, qscale):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("waves,min_cps", [(8, 1), (4, 2), (8, 3)])
+@pytest.mark.parametrize("T", [1, 127, 128, 129, 511, 512, 513, 2048, 4096, 4097])
+def test_attention_decode_launch_shapes_vs_fp64(kv_cache, T, waves, min_cps):
+    """The tuning launch shapes: 8 waves (128-position chunks) and several
+    chunks per split, against the fp64 attention (qscale 4)."""
+    max_ctx, kc, vc, dkc, dvc = kv_cache
+    q = (arc.synth_normal(SEED, 20 + T, KVH * HPK * 128) * 4.0).astype(np.float32)
+    out = arc.DeviceBuffer(q.nbytes)
+    ws = arc.DeviceBuffer(arc.attention_workspace_bytes(KVH, HPK))
+    arc.tune_attention(waves, min_cps)
+    try:
+        arc.attention_decode(dev(q), dkc, dvc, KVH, HPK, max_ctx, T, out, ws)
+    finally:
+        arc.tune_attention(0, 0)
+    err = orc.rel_err(out.download(np.float32), orc.attention_decode_f64(q, kc, vc, T, KVH * HPK, KVH))
+    print(f"T={T} waves={waves} min_cps={min_cps}: per-element error {err:.3g}", flush=True)
+    assert err <= TOL
+
+
+def test_attention_tuning_rejects_bad_shapes():
+    for waves, cps in ((16, 0), (3, 0), (0, -1)):
+        with pytest.raises(arc.ArcError):
+            arc.tune_attention(waves, cps)
+
+
 def test_attention_decode_repeatable_and_rejects_bad_context(kv_cache):
     """Two calls give identical outputs (fixed reduction order, counters
     reset by the call); T = 0 and T > max_ctx are refused."""
