@@ -65,6 +65,7 @@ static_assert(kChunk == 4 * kAttnTile, "the session's chunk: 4 waves of 16 posit
 static_assert(kHeadDim == 2 * kWave, "V sum: one dim pair per lane");
 static_assert(kMaxSplits <= kWave, "the merge takes one split per lane");
 constexpr int kAttnMergeBatch = 16;  // split outputs loaded per batch in the merge
+constexpr int kCpolSc1 = 16;         // buffer-load cache policy bit sc1 (device-coherent read)
 // Splits that load their first chunk before reading the position: with 4
 // waves, splits 0..7 take part in every plan above 448 positions; with 8,
 // splits 0..3 (plans above 384 positions).
@@ -284,12 +285,12 @@ __global__ __launch_bounds__(W * kWave) void k_attn(AttnParams a)
         return;
     }
     // this split's partials, written past the L2 for the merging workgroup
+    // (16-byte buffer stores with the cache policy of st_agent)
     if (owner) {
-        float* po = a.po + ((base + s) * HPK + hh) * kHeadDim + 4 * dq4;
-        st_agent(po, osp.x);
-        st_agent(po + 1, osp.y);
-        st_agent(po + 2, osp.z);
-        st_agent(po + 3, osp.w);
+        const __amdgpu_buffer_rsrc_t pws = __builtin_amdgcn_make_buffer_rsrc(
+            a.po + (base + s) * HPK * kHeadDim, 0, int(HPK * kHeadDim * 4), 0x00020000);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, osp), pws, (hh * kHeadDim + 4 * dq4) * 4u, 0,
+                                               kCpolSc1);
         if (dq4 == 0) {
             st_agent(a.pml + ((base + s) * HPK + hh) * 2, Msp);
             st_agent(a.pml + ((base + s) * HPK + hh) * 2 + 1, Lsp);
@@ -300,8 +301,9 @@ __global__ __launch_bounds__(W * kWave) void k_attn(AttnParams a)
     // merge (last workgroup of kv head g).  Wave w, lane = split: the split
     // weights w_s = e^(m_s - M) / L of heads w, w + W (M and L by wave
     // reductions) into LDS; then thread -> (head hh, dims 4dq4 .. +3) sums
-    // the splits' o weighted, in split order, loads in batches of kB (the
-    // first batch is issued right after the (m, l) loads).
+    // the splits' o weighted, in split order, loads in batches of kB, two
+    // batches in flight (the first two are issued right after the (m, l)
+    // loads).
     const bool in = uint32_t(lane) < sp.nsplit;
     const uint32_t ss = min(uint32_t(lane), sp.nsplit - 1);
     float2 ml[2];  // at most 2 heads per wave (W >= 4)
@@ -311,18 +313,26 @@ __global__ __launch_bounds__(W * kWave) void k_attn(AttnParams a)
         const uint32_t h = min(uint32_t(w + W * k), uint32_t(HPK - 1));
         ml[k] = ld_agent2(a.pml + ((base + ss) * HPK + h) * 2);
     }
-    const float* src = a.po + (base * HPK + hh) * kHeadDim + 4 * dq4;
+    // the kv head's partials as a buffer resource: 16-byte loads with the
+    // device-coherence cache policy of ld_agent (sc1: not served from a
+    // possibly stale cache line)
+    const float* src = a.po + base * HPK * kHeadDim;
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src), 0, int(kMaxSplits * HPK * kHeadDim * 4), 0x00020000);
+    const uint32_t off0 = (hh * kHeadDim + 4 * dq4) * 4u;
     constexpr int kB = kAttnMergeBatch;
-    float4 ov[kB];
-    auto fetch = [&](uint32_t s0) {
+    float4 ova[kB], ovb[kB];  // two batches: the next one's loads in flight while one is summed
+    auto fetch = [&](float4 (&ov)[kB], uint32_t s0) {
 #pragma unroll
         for (int u = 0; u < kB; ++u) {
-            const float* p = src + uint64_t(min(s0 + u, sp.nsplit - 1)) * HPK * kHeadDim;
-            const float2 lo = ld_agent2(p), hi = ld_agent2(p + 2);
-            ov[u] = make_float4(lo.x, lo.y, hi.x, hi.y);
+            const uint32_t off = off0 + min(s0 + u, sp.nsplit - 1) * uint32_t(HPK * kHeadDim * 4);
+            ov[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, kCpolSc1));
         }
     };
-    if (owner) fetch(0);
+    if (owner) {
+        fetch(ova, 0);
+        if (uint32_t(kB) < sp.nsplit) fetch(ovb, kB);
+    }
 #pragma unroll
     for (int k = 0; k < kMH; ++k) {
         const int h = w + W * k;
@@ -337,8 +347,7 @@ __global__ __launch_bounds__(W * kWave) void k_attn(AttnParams a)
     __syncthreads();
     if (owner) {
         float4 r = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (uint32_t s0 = 0; s0 < sp.nsplit; s0 += kB) {
-            if (s0 != 0) fetch(s0);
+        auto sum = [&](const float4 (&ov)[kB], uint32_t s0) {
 #pragma unroll
             for (int u = 0; u < kB; ++u)
                 if (s0 + u < sp.nsplit) {
@@ -348,6 +357,15 @@ __global__ __launch_bounds__(W * kWave) void k_attn(AttnParams a)
                     r.z = __builtin_fmaf(ov[u].z, f, r.z);
                     r.w = __builtin_fmaf(ov[u].w, f, r.w);
                 }
+        };
+        // batches s0 (in ova) and s0 + kB (in ovb) are in flight on entry
+        for (uint32_t s0 = 0; s0 < sp.nsplit; s0 += 2 * kB) {
+            sum(ova, s0);
+            if (s0 + 2 * kB < sp.nsplit) fetch(ova, s0 + 2 * kB);
+            if (s0 + kB < sp.nsplit) {
+                sum(ovb, s0 + kB);
+                if (s0 + 3 * kB < sp.nsplit) fetch(ovb, s0 + 3 * kB);
+            }
         }
         reinterpret_cast<float4*>(out + hh * kHeadDim)[dq4] = r;
     }
