@@ -10,20 +10,26 @@ timing; the step rotates over `--banks` copies of the weights (default 8,
 1.07 GB) so the 256 MB Infinity Cache cannot serve them.
 
 value = algorithmic bytes per step (weights + x/s/y reads and writes,
-132,257,792 B) / time, in GB/s.  Both kernels of the step are timed alone with
-HIP events on their stream (K back-to-back launches over the weight banks,
-median of three loops after a warm-up); the roofline object is the longer of
-the two.  Config 0 (the gate GEMV) and config 2 (RMSNorm + LM head + argmax)
-are timed the same way, the 28-layer decode (config 3) and the 256-token
-prompt pass (config 4) on the 7B-shaped model.  cpu_baseline times the
-oracle's serial-fp32 restatement of the reference CPU kernels on the same FFN
-block (bounded sample; 1 thread, and every thread the box gives the process).
+132,257,792 B) / time, in GB/s, after a warm-up that runs until the clocks
+settle (1 s).  Both kernels of the step are timed alone with HIP events on
+their stream (max(K, 200) back-to-back launches over the weight banks,
+median of three loops after a warm-up; their sum is reported next to the
+step); the roofline object is the longer of the two.  Config 0 (the gate GEMV) and config 2 (RMSNorm +
+LM head + argmax) are timed over max(K, 200) back-to-back launches (median
+of three loops), the 28-layer decode (config 3) and the 256-token prompt
+pass (config 4) on the 7B-shaped model.  stream_ceiling is a plain
+streaming read (1, 2, 4 or 8 loads per lane in flight) at the same bytes.
+cpu_baseline times the oracle's serial-fp32 restatement of the reference CPU
+kernels on the same FFN block, the gate GEMV, the LM head and one decode
+step at 512 positions (bounded samples; 1 thread, and every thread the box
+gives the process).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -76,32 +82,112 @@ def time_loop(fn, iters: int, stream: arc.Stream) -> float:
 
 def cpu_baseline(sample_reps: int) -> dict:
     """The oracle's serial-fp32 restatement of the reference CPU kernels
-    (per-element decode, one row at a time) on the same FFN block."""
+    (per-element decode, one row at a time; src/sa1_component_benchmark.cpp
+    :165-173) timed on this box's host cores, at 1 thread and at every thread
+    the box gives the process: config 1 (the FFN block: the headline sample),
+    config 0 (the gate GEMV), config 2 (RMSNorm + LM head + argmax) and one
+    decode step at 512 cached positions (a bounded sample: one of the 28
+    layers, scaled to 28, plus the LM head)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as orc  # the checker; used here only as the CPU baseline
 
+    O = orc.oracle()
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    # every thread the box gives this process: its affinity set, capped by the
+    # OpenMP thread count the box sets (its CPU share)
+    ncores = max(1, min(nproc, int(os.environ.get("OMP_NUM_THREADS", nproc))))
+
+    def timed(fn, reps: int, warm: bool = True) -> tuple:
+        """Median seconds of fn(threads) at 1 and at ncores threads (after one
+        warm-up run each when `warm`)."""
+        out = []
+        for th in (1, ncores):
+            if warm:
+                fn(th)
+            out.append(sorted(_wall(fn, th) for _ in range(reps))[reps // 2])
+        return tuple(out)
+
+    def _wall(fn, th) -> float:
+        t0 = time.perf_counter()
+        fn(th)
+        return time.perf_counter() - t0
+
+    def rms(x, w, eps=1e-6):
+        y = np.empty_like(x)
+        O.orc_rmsnorm_f32(x.ctypes.data, w.ctypes.data, x.size, C.c_float(eps), y.ctypes.data)
+        return y
+
+    def swiglu(g, u):
+        o = np.empty_like(g)
+        O.orc_swiglu_f32(g.ctypes.data, u.ctypes.data, g.size, o.ctypes.data)
+        return o
+
+    # config 1: the FFN block
     wg = arc.synth_packed(arc.Q4_K, SEED, 1, FFN, H)
     wu = arc.synth_packed(arc.Q4_K, SEED, 2, FFN, H)
     wd = arc.synth_packed(arc.Q6_K, SEED, 3, H, FFN)
     x = arc.synth_normal(SEED, 4, H)
 
-    def step(threads: int) -> float:
-        t0 = time.perf_counter()
-        g = orc.gemv_r0(arc.Q4_K, wg, FFN, H, x, threads=threads)
-        u = orc.gemv_r0(arc.Q4_K, wu, FFN, H, x, threads=threads)
-        s = np.empty_like(g)
-        orc.oracle().orc_swiglu_f32(g.ctypes.data, u.ctypes.data, FFN, s.ctypes.data)
-        orc.gemv_r0(arc.Q6_K, wd, H, FFN, s, threads=threads)
-        return time.perf_counter() - t0
+    def ffn(th: int) -> None:
+        g = orc.gemv_r0(arc.Q4_K, wg, FFN, H, x, threads=th)
+        u = orc.gemv_r0(arc.Q4_K, wu, FFN, H, x, threads=th)
+        orc.gemv_r0(arc.Q6_K, wd, H, FFN, swiglu(g, u), threads=th)
 
-    step(1)  # warmup
-    t1 = sorted(step(1) for _ in range(sample_reps))[sample_reps // 2]
-    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-    # every thread the box gives this process: its affinity set, capped by the
-    # OpenMP thread count the box sets (its CPU share)
-    ncores = max(1, min(nproc, int(os.environ.get("OMP_NUM_THREADS", nproc))))
-    step(ncores)
-    tn = sorted(step(ncores) for _ in range(sample_reps))[sample_reps // 2]
+    t1, tn = timed(ffn, sample_reps)
+
+    # config 0: the gate GEMV
+    g1, gn = timed(lambda th: orc.gemv_r0(arc.Q4_K, wg, FFN, H, x, threads=th), sample_reps)
+
+    # config 2: RMSNorm + Q6_K LM head [152064 x 3584] + argmax
+    wlm = arc.synth_packed(arc.Q6_K, SEED, 5, VOC, H)
+    hh = arc.synth_normal(SEED, 6, H)
+    nw = arc.synth_normal(SEED, 7, H, 1.0, 0.05)
+
+    def head(th: int) -> int:
+        logits = orc.gemv_r0(arc.Q6_K, wlm, VOC, H, rms(hh, nw), threads=th)
+        return int(orc.top2(logits).top1)
+
+    l1, ln = timed(head, 1, warm=False)
+
+    # one decode step at 512 cached positions: one layer in fp32 (attention
+    # through the oracle's restatement, fp16 cache rows), then the LM head;
+    # step = 28 x (one layer) + LM head
+    d = arc.qwen25_7b_dims()
+    kvd = d.kv_heads * d.head_dim
+    ctx = 512
+    wq = arc.synth_packed(arc.Q4_K, SEED, 20, H, H)
+    wk = arc.synth_packed(arc.Q4_K, SEED, 21, kvd, H)
+    wv = arc.synth_packed(arc.Q6_K, SEED, 22, kvd, H)
+    wo = arc.synth_packed(arc.Q4_K, SEED, 23, H, H)
+    bq, bk, bv = (arc.synth_normal(SEED, 24 + i, n, 0.0, 0.1) for i, n in enumerate((H, kvd, kvd)))
+    an, fn_ = arc.synth_normal(SEED, 27, H, 1.0, 0.05), arc.synth_normal(SEED, 28, H, 1.0, 0.05)
+    kc = arc.synth_normal(SEED, 29, (ctx + 1) * kvd).astype(np.float16)
+    vc = arc.synth_normal(SEED, 30, (ctx + 1) * kvd).astype(np.float16)
+
+    def layer(th: int) -> None:
+        h = x.copy()
+        for _ in range(1):
+            xn = rms(h, an)
+            q = orc.gemv_r0(arc.Q4_K, wq, H, H, xn, bq, threads=th)
+            k = orc.gemv_r0(arc.Q4_K, wk, kvd, H, xn, bk, threads=th)
+            v = orc.gemv_r0(arc.Q6_K, wv, kvd, H, xn, bv, threads=th)
+            O.orc_rope_f32(q.ctypes.data, d.q_heads, d.head_dim, ctx, C.c_float(d.rope_theta))
+            O.orc_rope_f32(k.ctypes.data, d.kv_heads, d.head_dim, ctx, C.c_float(d.rope_theta))
+            kc[ctx * kvd:(ctx + 1) * kvd] = k.astype(np.float16)
+            vc[ctx * kvd:(ctx + 1) * kvd] = v.astype(np.float16)
+            att = orc.attention_decode_f64(q, kc, vc, ctx + 1, d.q_heads, d.kv_heads).astype(np.float32)
+            h = h + orc.gemv_r0(arc.Q4_K, wo, H, H, att, threads=th)
+            xn = rms(h, fn_)
+            s = swiglu(orc.gemv_r0(arc.Q4_K, wg, FFN, H, xn, threads=th),
+                       orc.gemv_r0(arc.Q4_K, wu, FFN, H, xn, threads=th))
+            h = h + orc.gemv_r0(arc.Q6_K, wd, H, FFN, s, threads=th)
+
+    y1, yn = timed(layer, 1, warm=False)
+    step1 = d.layers * y1 + l1
+    stepn = d.layers * yn + ln
+    per_core = lambda nbytes, t1_, tn_: {  # noqa: E731
+        "1_core": {"GB/s": round(nbytes / t1_ / 1e9, 4), "ms": round(t1_ * 1e3, 2)},
+        f"{ncores}_cores": {"GB/s": round(nbytes / tn_ / 1e9, 4), "ms": round(tn_ * 1e3, 2)}}
     return {
         "value": round(BYTES_STEP / t1 / 1e9, 4),
         "unit": "GB/s",
@@ -112,6 +198,13 @@ def cpu_baseline(sample_reps: int) -> dict:
         "ms_per_step": round(t1 * 1e3, 2),
         "all_cores": {"cores": ncores, "nproc": nproc, "value": round(BYTES_STEP / tn / 1e9, 4),
                       "ms_per_step": round(tn * 1e3, 2)},
+        "config0_q4k_gate_gemv": per_core(BYTES_GATE, g1, gn),
+        "config2_lmhead_argmax": per_core(BYTES_LM, l1, ln),
+        "decode_step_512": {
+            "sample": "one layer of the 7B shape in fp32 (attention at 512 positions through the oracle's "
+                      "restatement) scaled to 28 layers, + RMSNorm/LM head/argmax; one run each",
+            "1_core": {"tokens_per_s": round(1.0 / step1, 4), "ms_per_token": round(step1 * 1e3, 1)},
+            f"{ncores}_cores": {"tokens_per_s": round(1.0 / stepn, 4), "ms_per_token": round(stepn * 1e3, 1)}},
     }
 
 
@@ -201,25 +294,27 @@ def load_traffic() -> dict:
         return json.load(f)
 
 
-def ceiling(nbytes: int, banks: int, stream: arc.Stream, iters: int) -> float:
+def ceiling(nbytes: int, banks: int, stream: arc.Stream, iters: int) -> tuple:
     """Streaming-read ceiling at `nbytes` per launch, rotating over `banks`
-    initialised buffers: arc_probe_read (one coalesced 16 B load per lane per
-    iteration) at 2048 / 4096 / 8192 workgroups, best of the three."""
+    initialised buffers: arc_probe_read_unrolled (coalesced 16 B loads, 1, 2,
+    4 or 8 independent loads per lane in flight) at 2048 / 4096 / 8192
+    workgroups.  Returns (best GB/s, {loads: best GB/s over the grids})."""
     n = nbytes // 4096 * 4096
     bufs = [arc.DeviceBuffer(n) for _ in range(banks)]
     for b in bufs:
         arc.check(arc.lib().arc_memset(b.ptr, 1, n, stream.handle))
     out = arc.DeviceBuffer(8192 * 256 * 4)
-    best = 0.0
-    for grid in (2048, 4096, 8192):
-        fn = lambda i: arc.probe_read(bufs[i % banks], n, out, grid, stream)  # noqa: E731
-        time_loop(fn, 10, stream)
-        ms = time_loop(fn, iters, stream)
-        best = max(best, n / (ms / 1e3) / 1e9)
+    per = {}
+    for loads in (1, 2, 4, 8):
+        for grid in (2048, 4096, 8192):
+            fn = lambda i: arc.probe_read_unrolled(bufs[i % banks], n, out, grid, loads, stream)  # noqa: E731
+            time_loop(fn, 20, stream)
+            ms = time_loop(fn, iters, stream)
+            per[loads] = max(per.get(loads, 0.0), n / (ms / 1e3) / 1e9)
     for b in bufs:
         b.close()
     out.close()
-    return best
+    return max(per.values()), {str(k): round(v, 1) for k, v in per.items()}
 
 
 def kernel_entry(name: str, nbytes: int, ms: float, traffic: dict) -> dict:
@@ -240,8 +335,8 @@ def components(banks: list, B: int, x, s, stream: arc.Stream, steps: int) -> dic
     def gate(i: int) -> None:
         arc.gemv(arc.Q4_K, banks[i % B][0], FFN, H, x, s, stream=stream)
 
-    time_loop(gate, 50, stream)
-    gate_ms = sorted(time_loop(gate, steps, stream) for _ in range(3))[1]
+    time_loop(gate, 200, stream)
+    gate_ms = sorted(time_loop(gate, max(steps, 200), stream) for _ in range(3))[1]
     comp["config0_q4k_gate_gemv"] = {"workload": "Q4_K GEMV [18944x3584], x fp32 [3584] -> y fp32 [18944]",
                                      "algorithmic_bytes": BYTES_GATE, "us": round(gate_ms * 1e3, 3),
                                      "GB/s": round(BYTES_GATE / (gate_ms / 1e3) / 1e9, 1),
@@ -264,8 +359,7 @@ def components(banks: list, B: int, x, s, stream: arc.Stream, steps: int) -> dic
 
     # the weights were generated on the host meanwhile: warm up for ~40 ms
     time_loop(head, 400, stream)
-    n = max(steps // 4, 10)
-    lm_ms = sorted(time_loop(head, n, stream) for _ in range(3))[1]
+    lm_ms = sorted(time_loop(head, max(steps, 200), stream) for _ in range(3))[1]
     comp["config2_lmhead_argmax"] = {"workload": "RMSNorm + Q6_K LM head [152064x3584] (held as padded blocks) "
                                                  "+ argmax (two launches)",
                                      "algorithmic_bytes": BYTES_LM, "us": round(lm_ms * 1e3, 3),
@@ -346,6 +440,23 @@ def main() -> int:
         arc.gateup_swiglu(arc.Q4_K, g, u, FFN, H, x, s, stream)
         arc.gemv_splitk(arc.Q6_K_PADDED, d, H, FFN, SPLITS, s, part, y, stream=stream)
 
+    log(f"warmup {args.warmup}, then until the clocks settle (1 s)")
+    time_loop(ffn_step, max(args.warmup, 1), stream)
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < 1.0:
+        time_loop(ffn_step, 50, stream)
+    arc.synchronize()
+    log(f"timing {args.steps} steps")
+    ms = time_loop(ffn_step, args.steps, stream)
+    arc.synchronize()
+    gbs = BYTES_STEP / (ms / 1e3) / 1e9
+
+    # each kernel of the step alone, back to back on the step's stream (the
+    # launch latency hidden behind the previous launch, as in the step):
+    # warmed up, then the median of three loops of max(K, 200) launches.
+    # (HIP events recorded between the kernels inside the step were tried:
+    # each record stalls the queue, the step grew from 34.0 to 45.1 us and
+    # the kernels' shares with it.)
     def gateup(i: int) -> None:
         g, u, _ = banks[i % B]
         arc.gateup_swiglu(arc.Q4_K, g, u, FFN, H, x, s, stream)
@@ -354,24 +465,14 @@ def main() -> int:
         _, _, d = banks[i % B]
         arc.gemv_splitk(arc.Q6_K_PADDED, d, H, FFN, SPLITS, s, part, y, stream=stream)
 
-    log(f"warmup {args.warmup}")
-    time_loop(ffn_step, max(args.warmup, 1), stream)
-    arc.synchronize()
-    log(f"timing {args.steps} steps")
-    ms = time_loop(ffn_step, args.steps, stream)
-    arc.synchronize()
-    gbs = BYTES_STEP / (ms / 1e3) / 1e9
-
-    # each kernel of the step back to back on its stream (launch latency
-    # hidden behind the previous launch, as in the step): warmed up until the
-    # clocks settle, then the median of three timed loops of K launches
-    time_loop(gateup, max(args.warmup, 50), stream)
-    ms_gu = sorted(time_loop(gateup, args.steps, stream) for _ in range(3))[1]
-    time_loop(down, max(args.warmup, 50), stream)
-    ms_dn = sorted(time_loop(down, args.steps, stream) for _ in range(3))[1]
+    n_k = max(args.steps, 200)
+    time_loop(gateup, 200, stream)
+    ms_gu = sorted(time_loop(gateup, n_k, stream) for _ in range(3))[1]
+    time_loop(down, 200, stream)
+    ms_dn = sorted(time_loop(down, n_k, stream) for _ in range(3))[1]
     log(f"step {ms * 1e3:.2f} us ({gbs:.1f} GB/s); gate/up {ms_gu * 1e3:.2f} us "
         f"({BYTES_GATEUP / (ms_gu / 1e3) / 1e9:.1f} GB/s); down split-K {ms_dn * 1e3:.2f} us "
-        f"({BYTES_DOWN / (ms_dn / 1e3) / 1e9:.1f} GB/s)")
+        f"({BYTES_DOWN / (ms_dn / 1e3) / 1e9:.1f} GB/s); sum {(ms_gu + ms_dn) * 1e3:.2f} us")
 
     traffic = load_traffic()
     kernels = {"gateup_swiglu": kernel_entry("gateup_swiglu", BYTES_GATEUP, ms_gu, traffic),
@@ -379,12 +480,15 @@ def main() -> int:
     dominant = "gateup_swiglu" if ms_gu >= ms_dn else "down_splitk"
     roof = dict(kernels[dominant])
     roof["role"] = f"{dominant}: the longest kernel of the timed step"
+    roof["timing"] = (f"HIP events on the kernel's stream around {n_k} back-to-back launches (median of 3 "
+                      f"loops); gate/up {ms_gu * 1e3:.2f} + down {ms_dn * 1e3:.2f} = "
+                      f"{(ms_gu + ms_dn) * 1e3:.2f} us against the {ms * 1e3:.2f} us step")
 
     # practical read ceiling of this box at the same byte counts, same rotation
-    ceil_step = ceiling(BYTES_STEP, B, stream, args.steps)
-    ceil_dom = ceiling(roof["algorithmic_bytes_per_launch"], B, stream, args.steps)
-    log(f"stream-read ceiling: {ceil_step:.0f} GB/s at {BYTES_STEP} B, {ceil_dom:.0f} GB/s at "
-        f"{roof['algorithmic_bytes_per_launch']} B")
+    ceil_step, ceil_step_per = ceiling(BYTES_STEP, B, stream, max(args.steps, 200))
+    ceil_dom, ceil_dom_per = ceiling(roof["algorithmic_bytes_per_launch"], B, stream, max(args.steps, 200))
+    log(f"stream-read ceiling: {ceil_step:.0f} GB/s at {BYTES_STEP} B {ceil_step_per}, {ceil_dom:.0f} GB/s at "
+        f"{roof['algorithmic_bytes_per_launch']} B {ceil_dom_per}")
 
     result = {
         "metric": "Q4_K/Q6_K GEMV HBM GB/s (% of peak); 7B-shape decode tokens/s, 1 MI355X",
@@ -410,10 +514,13 @@ def main() -> int:
         "roofline": roof,
         "kernels": kernels,
         "stream_ceiling": {
-            "kernel": "arc_probe_read (coalesced 16 B/lane streaming read of initialised buffers, same bank "
-                      "rotation, best of 2048/4096/8192 workgroups)",
+            "kernel": "arc_probe_read_unrolled (coalesced 16 B/lane streaming read of initialised buffers, 1/2/4/8 "
+                      "independent loads per lane in flight, same bank rotation, best of 2048/4096/8192 "
+                      "workgroups)",
             "GB/s_at_step_bytes": round(ceil_step, 1),
+            "GB/s_at_step_bytes_by_loads_in_flight": ceil_step_per,
             "GB/s_at_roofline_kernel_bytes": round(ceil_dom, 1),
+            "GB/s_at_roofline_kernel_bytes_by_loads_in_flight": ceil_dom_per,
             "value_frac_of_ceiling": round(gbs / ceil_step, 4),
             "roofline_frac_of_ceiling": round(roof["achieved"] / ceil_dom, 4),
         },

@@ -262,6 +262,11 @@ int arc_tune_attention(int waves, int min_chunks_per_split);
  * workgroups of 256 lanes, 16 bytes per lane access, xor-folded into
  * out[grid*256] (device).  Measures the practical HBM read ceiling. */
 int arc_probe_read(const void *p, size_t bytes, uint32_t *out, uint32_t grid, arc_stream_t stream);
+/* The same probe with `loads` (1, 2, 4 or 8) independent 16-byte loads per
+ * lane in flight per iteration.  No counterpart in the reference: a
+ * measurement aid of this build. */
+int arc_probe_read_unrolled(const void *p, size_t bytes, uint32_t *out, uint32_t grid, int loads,
+                            arc_stream_t stream);
 
 /* ------------------------------------------------------ synthetic inputs */
 /* Host-side, deterministic generators for seeded synthetic packed tensors
