@@ -359,3 +359,51 @@ def simulate_rs(rows: int, K: int, epi: int, norm: bool, gx: int | None = None, 
                 row = gw + ti * stride
                 rep.check("output store", np.array([row]), np.array([row + 1]), 0, rows)
     return rep
+
+
+# ------------------------------------------------- embedding row and argmax tail
+def simulate_embed(nb: int, emb_rows: int, tokens, mistake: str | None = None) -> Report:
+    """Bounds model of the F_EMBED staging (arc_gemv.hpp gemv_body /
+    stage_x_rms / emb_group): for each token id the device may hold in
+    ctl->token, the row the launch decodes (erow = emb + (token < emb_rows ?
+    token : 0) * nb * 144), every byte emb_group reads for every group of
+    the row (d, dmin, the 12 scale bytes, 16 nibble bytes) and the raw row
+    workgroup 0 writes to h_out.  `mistake` = "token" drops the clamp."""
+    rep = Report()
+    table = emb_rows * nb * 144
+    gi = np.arange(nb * 16)
+    e = (gi >> 4) * KQK + x_group_offset(Q4, (gi >> 2) & 3, gi & 3)
+    for tok in tokens:
+        row = tok if mistake == "token" else (tok if tok < emb_rows else 0)
+        base = row * nb * 144
+        b = base + (e >> 8) * 144
+        rep.check("embedding header read", b, b + 16, 0, table)
+        k0 = e & 255
+        l64 = k0 & 63
+        nib = b + 16 + (k0 >> 6) * 32 + (l64 & 31)
+        rep.check("embedding nibble read", nib, nib + 16, 0, table)
+        rep.check("raw row store (h_out)", e, e + 16, 0, nb * KQK)
+    return rep
+
+
+def simulate_argnext(rows: int, n: int, best_len: int, out_cap: int, steps, idx_values,
+                     mistake: str | None = None) -> Report:
+    """Bounds model of argmax_finish (F_ARGNEXT): the last workgroup reads the
+    n per-workgroup bests (i = thread, thread + NT, ... < n) from a buffer of
+    best_len entries, turns the folded index into the token (idx < rows, else
+    0), and writes out_tokens[step] only while step < out_cap.  `mistake` =
+    "step" drops the out_cap check, "idx" the token clamp."""
+    rep = Report()
+    for NT in (256, 512):
+        t = np.arange(NT)
+        for k in range(-(-n // NT)):
+            i = t + k * NT
+            i = i[i < n]
+            rep.check("per-workgroup best load", i, i + 1, 0, best_len)
+    for step in steps:
+        if mistake == "step" or step < out_cap:
+            rep.check("out_tokens store", np.array([step]), np.array([step + 1]), 0, out_cap)
+    for idx in idx_values:
+        tok = idx if mistake == "idx" else (idx if idx < rows else 0)
+        rep.check("next token (embedding row of the next step)", np.array([tok]), np.array([tok + 1]), 0, rows)
+    return rep

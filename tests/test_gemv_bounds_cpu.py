@@ -4,8 +4,11 @@ blocks) and EXEC148, over grids from one workgroup to one wave tile per wave,
 and over the Q6_K layouts with four rows per lane that the library refuses to
 launch (one of them, k_gemv<Q6_K, 2, 4, PLAIN, 4>, took a GPU memory fault
 once at 301 x 3584): every weight read, epilogue load, x pre-load and x
-staging access, LDS access and store stays inside its buffer.  A mistake
-planted in the model (an unclamped row or block index) is reported."""
+staging access, LDS access and store stays inside its buffer.  Also the
+row-stream kernel, the F_EMBED embedding-row decode (every token id the
+control block can hold) and the F_ARGNEXT argmax tail (best loads,
+out_tokens stores, the next token).  A mistake planted in the model (an
+unclamped row, block, token or step index) is reported."""
 import itertools
 
 import pytest
@@ -125,3 +128,31 @@ def test_row_stream_planted_mistake_is_reported(mistake):
     # 2 super-blocks: owner lanes of blocks 2 .. 13 sit past the row
     r = gb.simulate_rs(37, 512, gb.PLAIN, False, 2, mistake=mistake)
     assert r.violations
+
+
+def test_embedding_row_decode_stays_in_bounds():
+    """F_EMBED: every token id the control block can hold -- in range, the
+    last row, one past it and the largest uint32 -- decodes inside the
+    token table; the raw row stays inside h_out."""
+    for nb, rows in ((14, 152064), (2, 4096), (1, 1)):
+        r = gb.simulate_embed(nb, rows, [0, 1, rows - 1, rows, rows + 7, 2**32 - 1])
+        assert r.checked > 0
+        assert not r.violations, (nb, rows, r.violations)
+
+
+def test_argmax_tail_stays_in_bounds():
+    """F_ARGNEXT: the best-of-workgroup loads, the out_tokens store at every
+    step up to past the cap, and the token handed to the next step."""
+    for rows, n in ((152064, 1024), (4096, 37), (5, 1)):
+        r = gb.simulate_argnext(rows, n, n, 64, range(0, 70), [0, rows - 1, rows, 2**32 - 1])
+        assert not r.violations, (rows, n, r.violations)
+
+
+@pytest.mark.parametrize("mistake", ["token"])
+def test_embedding_planted_mistake_is_reported(mistake):
+    assert gb.simulate_embed(14, 100, [100], mistake).violations
+
+
+@pytest.mark.parametrize("mistake", ["step", "idx"])
+def test_argmax_tail_planted_mistake_is_reported(mistake):
+    assert gb.simulate_argnext(100, 10, 10, 64, range(0, 70), [0, 100], mistake).violations
