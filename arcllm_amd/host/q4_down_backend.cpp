@@ -82,15 +82,15 @@ namespace {
 // Future decode tokens from which each path pays for itself on MI355X,
 // measured with arcllm_q4_paths on the Qwen2.5-7B shape with the 14 Q4_K
 // ffn_down layers of its Q4_K_M file (family image 549,527,552 bytes):
-//   saving per decode token, route B over route A: 61.4 us (28-layer step,
-//     2.020 -> 1.959 ms at context 512);
-//   P1: allocation + GPU repack 1.55 ms, GPU validation 0.45 ms -> 33;
-//   P3: sidecar read (page cache dropped) + upload ~98 ms + validation -> 1600;
-//   P0: host repack (16 threads) + upload ~78 ms + validation -> 1300;
+//   saving per decode token, route B over route A: 12.1 us (28-layer step,
+//     1.603 -> 1.591 ms at context 512);
+//   P1: allocation + GPU repack 0.89 ms, GPU validation 0.39 ms -> 106;
+//   P3: sidecar read (page cache dropped) + upload ~100 ms + validation -> 8355;
+//   P0: host repack (16 threads) + upload ~65 ms + validation -> 5392;
 // threshold = ceil(cost / saving).  Profile 1 doubles profile 0, as the
 // reference's conservative profile roughly does (src/registrations/
 // arcllm_v1_q4k_down_reference_registration_v2.cpp:39-46: 2/4, 15/33, 17/37).
-constexpr std::array<std::uint64_t, 6> kThresholds = {33, 1600, 1300, 66, 3200, 2600};
+constexpr std::array<std::uint64_t, 6> kThresholds = {106, 8355, 5392, 212, 16710, 10784};
 
 constexpr reg::ProvenanceRef kMeasured{"profiles/q4_down_routes_mi355x.md", nullptr};
 constexpr auto V = reg::ValidationState::VALIDATED;
