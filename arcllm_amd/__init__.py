@@ -89,6 +89,7 @@ _SIGS = {
     "arc_tune_waves": [C.c_int],
     "arc_tune_rowstream": [C.c_int],
     "arc_tune_attention": [C.c_int, C.c_int],
+    "arc_tune_decode": [C.c_int, C.c_int, C.c_int, C.c_int],
     "arc_probe_read": [_P, C.c_size_t, _P, _U32, _P],
     "arc_probe_read_unrolled": [_P, C.c_size_t, _P, _U32, C.c_int, _P],
     "arc_exec148_materialize": [_P, _U32, _U32, _P, _P],
@@ -475,6 +476,15 @@ def tune_attention(waves: int = 0, min_chunks_per_split: int = 0) -> None:
     """Decode attention launch shape: waves per workgroup (4 or 8) and the
     least chunks of 16 * waves positions per split; 0 = automatic."""
     check(lib().arc_tune_attention(int(waves), int(min_chunks_per_split)))
+
+
+DEC_O, DEC_GATEUP, DEC_DOWN, DEC_LMHEAD = 0, 1, 2, 3
+
+
+def tune_decode(kind: int, bs: int = 0, rpl: int = 1, waves: int = 0) -> None:
+    """Layout / waves of one GEMV of decode steps captured later (kind DEC_*);
+    bs = 0 and waves = 0 keep the step's own."""
+    check(lib().arc_tune_decode(int(kind), int(bs), int(rpl), int(waves)))
 
 
 def tune_rowstream(mode: int) -> None:

@@ -381,6 +381,24 @@ __global__ __launch_bounds__(W * kWave) void k_attn(AttnParams a)
 inline thread_local int g_attn_waves = 0;    // 0: automatic
 inline thread_local int g_attn_min_cps = 0;  // 0: automatic
 
+// Per-launch layout overrides of the decode step's GEMVs (tuning), read when
+// a step is captured: 0 the o projection, 1 the fused gate/up, 2 the down
+// projection, 3 the LM head.  bs = 0 keeps the step's own layout, waves = 0
+// its own waves per workgroup.
+enum DecKind { kDecO = 0, kDecGateUp = 1, kDecDown = 2, kDecLmHead = 3, kDecKinds = 4 };
+inline thread_local Cfg g_dec_cfg[kDecKinds] = {};
+
+static Cfg dec_cfg(int kind, Cfg c)
+{
+    const Cfg& o = g_dec_cfg[kind];
+    if (o.bs) {
+        c.bs = o.bs;
+        c.rpl = o.rpl;
+    }
+    if (o.waves) c.waves = o.waves;
+    return c;
+}
+
 template <int HPK, int W>
 static void launch_attn_hpk(const AttnParams& ap, uint32_t kv_heads, hipStream_t st)
 {
@@ -526,7 +544,7 @@ int launch_lm_head(arc_session* S, const float* x, bool logits, hipStream_t st)
     p.ctl = S->ctl;
     p.out_tokens = S->out_tokens;
     p.out_cap = S->out_cap;
-    const Cfg c = choose_cfg(EPI_ARGMAX, d.vocab, H / kQK, 1);
+    const Cfg c = dec_cfg(kDecLmHead, choose_cfg(EPI_ARGMAX, d.vocab, H / kQK, 1));
     uint32_t gx = 0;
     const bool dry = g_dry_run;
     g_dry_run = true;  // size the grid first: every workgroup needs a partials slot
@@ -622,6 +640,7 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         // tokens/s over the 8 the standalone choice takes for 2048+ rows)
         Cfg ocfg = choose_cfg(EPI_PLAIN, H, H / kQK, 1);
         if (!g_force_waves) ocfg.waves = 4;
+        ocfg = dec_cfg(kDecO, ocfg);
         if ((rc = chk(launch_gemv_epi(EPI_PLAIN, kFmtQ4, ocfg, p, 1, st), "o projection")))
             return rc;
 
@@ -631,7 +650,9 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         p.normw = L.ffn_norm;
         p.eps = d.rms_eps;
         p.y = S->s;
-        if ((rc = chk(launch_gemv_epi(EPI_SWIGLU, kFmtQ4, choose_cfg(EPI_SWIGLU, F, H / kQK, 1), p, 1, st), "gate/up")))
+        if ((rc = chk(launch_gemv_epi(EPI_SWIGLU, kFmtQ4, dec_cfg(kDecGateUp, choose_cfg(EPI_SWIGLU, F, H / kQK, 1)), p,
+                                      1, st),
+                      "gate/up")))
             return rc;
 
         // down + residual: h = h1 + Wd s (route B: the layer's EXEC148 image)
@@ -643,7 +664,8 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         // padded Q6_K down: 16 quads per row, 8 waves (measured on the 7B shape,
         // 3584 x 18944: 14.9 vs 15.2 us for the automatic (8, 1); decode
         // +0.3 .. 0.6% tokens/s)
-        const Cfg dcfg = (dfmt == int(kFmtQ6P) && !g_force.bs) ? Cfg{16, 1, 8} : choose_cfg(EPI_PLAIN, H, F / kQK, 1);
+        const Cfg dcfg = dec_cfg(kDecDown, (dfmt == int(kFmtQ6P) && !g_force.bs) ? Cfg{16, 1, 8}
+                                                                                  : choose_cfg(EPI_PLAIN, H, F / kQK, 1));
         if ((rc = chk(launch_gemv_epi(EPI_PLAIN, dfmt, dcfg, p, 1, st), "down projection")))
             return rc;
     }
@@ -660,6 +682,19 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
 using namespace arc;
 
 extern "C" {
+
+int arc_tune_decode(int kind, int bs, int rpl, int waves)
+{
+    if (kind < 0 || kind >= kDecKinds) return set_error(ARC_ERR_INVALID_ARGUMENT, "decode launch kind must be 0..3");
+    if (waves != 0 && waves != 4 && waves != 8)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "waves per workgroup must be 0 (the step's own), 4 or 8");
+    static const int ok[][2] = {{1, 1}, {1, 2}, {1, 4}, {2, 1}, {2, 2}, {2, 4}, {4, 1}, {4, 2}, {8, 1}, {8, 2}, {16, 1}};
+    bool found = bs == 0;
+    for (const auto& c : ok) found = found || (c[0] == bs && c[1] == rpl);
+    if (!found) return set_error(ARC_ERR_INVALID_ARGUMENT, "no kernel instance for bs=%d rpl=%d", bs, rpl);
+    g_dec_cfg[kind] = Cfg{bs, bs ? rpl : 0, waves};
+    return ARC_OK;
+}
 
 int arc_tune_attention(int waves, int min_chunks_per_split)
 {

@@ -257,6 +257,11 @@ int arc_tune_rowstream(int mode);
  * thread: waves per workgroup (4 or 8; a chunk is 16 positions per wave)
  * and the least chunks one split (workgroup) covers; 0 = automatic. */
 int arc_tune_attention(int waves, int min_chunks_per_split);
+/* Tuning hook: the lane layout (bs quads per row, rpl rows per lane; bs = 0
+ * keeps the step's own) and waves per workgroup (0 = the step's own) of one
+ * GEMV of decode steps captured later on this host thread: kind 0 the o
+ * projection, 1 the fused gate/up, 2 the down projection, 3 the LM head. */
+int arc_tune_decode(int kind, int bs, int rpl, int waves);
 
 /* Diagnostic: streaming read of `bytes` (16-byte aligned) with `grid`
  * workgroups of 256 lanes, 16 bytes per lane access, xor-folded into
