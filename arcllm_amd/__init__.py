@@ -90,6 +90,7 @@ _SIGS = {
     "arc_tune_rowstream": [C.c_int],
     "arc_tune_attention": [C.c_int, C.c_int],
     "arc_tune_decode": [C.c_int, C.c_int, C.c_int, C.c_int],
+    "arc_tune_fuse_attn_o": [C.c_int],
     "arc_probe_read": [_P, C.c_size_t, _P, _U32, _P],
     "arc_probe_read_unrolled": [_P, C.c_size_t, _P, _U32, C.c_int, _P],
     "arc_exec148_materialize": [_P, _U32, _U32, _P, _P],
@@ -476,6 +477,12 @@ def tune_attention(waves: int = 0, min_chunks_per_split: int = 0) -> None:
     """Decode attention launch shape: waves per workgroup (4 or 8) and the
     least chunks of 16 * waves positions per split; 0 = automatic."""
     check(lib().arc_tune_attention(int(waves), int(min_chunks_per_split)))
+
+
+def tune_fuse_attn_o(on: bool = True) -> None:
+    """Attention and o projection of decode steps captured later as one
+    launch (default) or two."""
+    check(lib().arc_tune_fuse_attn_o(1 if on else 0))
 
 
 DEC_O, DEC_GATEUP, DEC_DOWN, DEC_LMHEAD = 0, 1, 2, 3

@@ -1,13 +1,15 @@
 // arc_decode.hip -- the single-token greedy decode step of a Qwen2.5-shaped
 // model on gfx950, and its model/session C ABI (include/arcllm_hip.h).
 //
-// One decode step (src/arcllm_v1_runtime.cpp:371-421 restated as 5 launches
+// One decode step (src/arcllm_v1_runtime.cpp:371-421 restated as 4 launches
 // per layer + 1 instead of 16 dispatches per layer + a host argmax):
 //   per layer  [attn RMSNorm + q/k GEMV + bias + RoPE + k -> fp16 cache  k_qkv<v format>
 //               and v GEMV + bias -> fp16 cache, one launch; layer 0
 //               decodes the token's embedding row while staging x]
-//              [cached GQA: chunk workgroups + last-arriver merge]       k_attn
-//              [o GEMV + residual]                                       k_gemv<Q4,EPI_PLAIN>
+//              [cached GQA: chunk workgroups + last-arriver merge, and   k_attn_o
+//               the o GEMV + residual, whose workgroups wait for the
+//               attention's output (two launches, k_attn and
+//               k_gemv<Q4,EPI_PLAIN>, when tuning asks for other shapes)]
 //              [ffn RMSNorm + gate/up GEMV + SwiGLU]                     k_gemv<Q4,EPI_SWIGLU>
 //              [down GEMV + residual]                                    k_gemv<down,EPI_PLAIN>
 //   head       [output RMSNorm + LM head + argmax; the last workgroup
@@ -41,6 +43,8 @@ struct AttnParams {
     uint32_t max_ctx;         // cache rows per layer (loads are clamped to it)
     uint32_t min_cps;         // chunks per split at least (>= 1)
     float scale;
+    uint32_t* done;           // in the launch fused with the o projection: kDoneCopies copies of a
+                              // counter raised once per kv head when its output is written (past the L2)
 };
 
 // Split plan of one decode position over T cached positions: chunks of
@@ -105,8 +109,10 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 // workgroup arrives last.
 // Semantics: src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1177-1212,
 // shaders/p7_attention_kv_online.comp (kv head = q head / (q_heads/kv_heads)).
-template <int HPK, int W>
-__global__ __launch_bounds__(W * kWave) void k_attn(AttnParams a)
+// Workgroup (s, g) of the attention; FUSED: the launch also runs the o
+// projection, which waits for a.done to count every kv head.
+template <int HPK, int W, bool FUSED>
+__device__ __forceinline__ void attn_body(const AttnParams& a, const uint32_t s, const uint32_t g)
 {
     constexpr int kC = W * kAttnTile;  // positions per chunk
     static_assert(W == 4 || W == 8, "4 or 8 waves per workgroup");
@@ -117,7 +123,6 @@ __global__ __launch_bounds__(W * kWave) void k_attn(AttnParams a)
     __shared__ float fw[kMaxSplits][HPK];                // merge: split weights
     __shared__ uint32_t flag;
 
-    const uint32_t s = blockIdx.x, g = blockIdx.y;
     const uint64_t kvd = uint64_t(a.kv_heads) * kHeadDim;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int r16 = lane & 15, grp = lane >> 4;  // scores: MFMA row/column, K-slot group
@@ -276,12 +281,25 @@ __global__ __launch_bounds__(W * kWave) void k_attn(AttnParams a)
     }
 
     float* out = a.out + uint64_t(g) * HPK * kHeadDim;
+    // the kv head's output; fused: written past the L2 (sc1) for the o
+    // projection's workgroups, then counted in
+    auto store_out = [&](float4 r) {
+        if constexpr (FUSED) {
+            const __amdgpu_buffer_rsrc_t ors =
+                __builtin_amdgcn_make_buffer_rsrc(out, 0, int(HPK * kHeadDim * 4), 0x00020000);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, r), ors, (hh * kHeadDim + 4 * dq4) * 4u,
+                                                   0, kCpolSc1);
+        } else {
+            reinterpret_cast<float4*>(out + hh * kHeadDim)[dq4] = r;
+        }
+    };
     const uint64_t base = uint64_t(g) * kMaxSplits;
     if (sp.nsplit == 1) {
         if (owner) {
             const float li = 1.0f / Lsp;
-            reinterpret_cast<float4*>(out + hh * kHeadDim)[dq4] = make_float4(osp.x * li, osp.y * li, osp.z * li, osp.w * li);
+            store_out(make_float4(osp.x * li, osp.y * li, osp.z * li, osp.w * li));
         }
+        if constexpr (FUSED) signal_done(a.done, kDoneCopies, kDoneStride);
         return;
     }
     // this split's partials, written past the L2 for the merging workgroup
@@ -367,8 +385,51 @@ __global__ __launch_bounds__(W * kWave) void k_attn(AttnParams a)
                 if (s0 + 3 * kB < sp.nsplit) fetch(ovb, s0 + 3 * kB);
             }
         }
-        reinterpret_cast<float4*>(out + hh * kHeadDim)[dq4] = r;
+        store_out(r);
     }
+    if constexpr (FUSED) signal_done(a.done, kDoneCopies, kDoneStride);
+}
+
+template <int HPK, int W>
+__global__ __launch_bounds__(W * kWave) void k_attn(AttnParams a)
+{
+    attn_body<HPK, W, false>(a, blockIdx.x, blockIdx.y);
+}
+
+// Attention and the o projection in one launch.  Workgroups [0, n_attn) are
+// the attention's (split b % kMaxSplits, kv head b / kMaxSplits), the rest
+// the o GEMV's: those load their first weights, wait until every kv head's
+// output is written (a.done = kv heads, each workgroup polling its own copy
+// of the counter), then stage it as x.  The o workgroups come after every
+// attention workgroup in dispatch order and the grid fits on the device at
+// once, so a waiting workgroup never holds back one it waits for.  The next
+// launch (the ffn gate/up) zeroes the done copies; a wait that gives up
+// counts in ctl->waits_expired, which the host reports as an error.
+struct AttnOWait {
+    static constexpr bool kWaits = true;
+    const uint32_t* done;
+    uint32_t n;
+    DecodeCtl* ctl;
+    __device__ void operator()() const
+    {
+        __shared__ uint32_t flag;
+        const bool ok = wait_count(done, n, &flag);
+        if (threadIdx.x == 0 && !ok)
+            __hip_atomic_fetch_add(&ctl->waits_expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+};
+constexpr int kAttnOBs = 8, kAttnORpl = 1;  // o projection layout in the fused launch (4 waves)
+
+template <int HPK>
+__global__ __launch_bounds__(4 * kWave) void k_attn_o(AttnParams a, GemvParams o, uint32_t n_attn)
+{
+    const uint32_t b = blockIdx.x;
+    if (b < n_attn) {
+        attn_body<HPK, 4, true>(a, b % kMaxSplits, b / kMaxSplits);
+        return;
+    }
+    const AttnOWait hook{a.done + ((b - n_attn) % kDoneCopies) * kDoneStride, a.kv_heads, o.ctl};
+    gemv_body<kFmtQ4, kAttnOBs, kAttnORpl, EPI_PLAIN, 4, AttnOWait>(o, b - n_attn, gridDim.x - n_attn, hook);
 }
 
 // Attention launch shape (tuning): waves per workgroup and the least chunks
@@ -431,6 +492,62 @@ static void launch_attn(AttnParams ap, uint32_t kv_heads, hipStream_t st)
         launch_attn_w<8>(ap, kv_heads, st);
     else
         launch_attn_w<4>(ap, kv_heads, st);
+}
+
+// Attention + o projection in one launch (k_attn_o): 1 automatic, 0 two
+// launches (tuning and comparison).
+inline thread_local int g_fuse_attn_o = 1;
+
+template <int HPK>
+static hipError_t launch_attn_o_hpk(const AttnParams& ap, GemvParams o, hipStream_t st, bool* done)
+{
+    *done = false;
+    const Cfg c{kAttnOBs, kAttnORpl, 4};
+    o.ntiles = (o.rows + tile_rows(c) - 1) / tile_rows(c);
+    const size_t lds = size_t(o.panel) * kXBlk * sizeof(float);
+    static int occ[kPanel + 1] = {};
+    if (!occ[o.panel]) {
+        int nb = 0;
+        if (lds > 65536)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_o<HPK>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_attn_o<HPK>, 4 * kWave, lds) != hipSuccess || nb < 1)
+            nb = 1;
+        occ[o.panel] = nb;
+    }
+    // every workgroup resident at once: the o part gets what the attention part leaves
+    const uint64_t n_attn = uint64_t(kMaxSplits) * ap.kv_heads;
+    const uint64_t resident = uint64_t(occ[o.panel]) * cu_count();
+    if (resident <= n_attn) return hipSuccess;  // not done: the caller launches the two kernels
+    const uint64_t n_o = std::min<uint64_t>(resident - n_attn, (o.ntiles + 3) / 4);
+    *done = true;
+    if (g_dry_run) return hipSuccess;
+    hipLaunchKernelGGL(k_attn_o<HPK>, dim3(uint32_t(n_attn + n_o)), dim3(4 * kWave), lds, st, ap, o,
+                       uint32_t(n_attn));
+    return hipGetLastError();
+}
+
+// Launches attention + o fused when the step's automatic shapes allow it
+// (4-wave attention, no layout override of the o projection); *done tells
+// whether it did.  The launch after it must zero ap.done's copies
+// (GemvParams::clear_done).
+static hipError_t launch_attn_o(AttnParams ap, const GemvParams& o, hipStream_t st, bool* done)
+{
+    *done = false;
+    if (!g_fuse_attn_o || (g_attn_waves && g_attn_waves != 4) || g_force_waves || g_force.bs ||
+        g_dec_cfg[kDecO].bs || g_dec_cfg[kDecO].waves)
+        return hipSuccess;
+    ap.min_cps = g_attn_min_cps > 0 ? uint32_t(g_attn_min_cps) : 1u;
+    switch (ap.hpk) {
+    case 1: return launch_attn_o_hpk<1>(ap, o, st, done);
+    case 2: return launch_attn_o_hpk<2>(ap, o, st, done);
+    case 3: return launch_attn_o_hpk<3>(ap, o, st, done);
+    case 4: return launch_attn_o_hpk<4>(ap, o, st, done);
+    case 5: return launch_attn_o_hpk<5>(ap, o, st, done);
+    case 6: return launch_attn_o_hpk<6>(ap, o, st, done);
+    case 7: return launch_attn_o_hpk<7>(ap, o, st, done);
+    default: return launch_attn_o_hpk<8>(ap, o, st, done);
+    }
 }
 
 static_assert(kMaxHpk == 8, "launch_attn instantiates 1..8");
@@ -629,20 +746,28 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         ap.hpk = d.q_heads / d.kv_heads;
         ap.max_ctx = S->max_ctx;
         ap.scale = 1.0f / std::sqrt(float(kHeadDim));
-        launch_attn(ap, d.kv_heads, st);
-        if ((rc = chk(hipGetLastError(), "attention"))) return rc;
+        ap.done = S->done;
 
         // o projection + residual: h1 = h + Wo attn
         p = make_params(kFmtQ4, L.o, nullptr, H, H, S->attn);
         p.res = S->h;
         p.y = S->h1;
-        // 4-wave workgroups for the o projection in the step (7B shape: +0.8-1.1%
-        // tokens/s over the 8 the standalone choice takes for 2048+ rows)
-        Cfg ocfg = choose_cfg(EPI_PLAIN, H, H / kQK, 1);
-        if (!g_force_waves) ocfg.waves = 4;
-        ocfg = dec_cfg(kDecO, ocfg);
-        if ((rc = chk(launch_gemv_epi(EPI_PLAIN, kFmtQ4, ocfg, p, 1, st), "o projection")))
+        p.ctl = S->ctl;
+        bool fused = false;
+        if ((rc = chk(launch_attn_o(ap, p, st, &fused), "attention + o projection")))
             return rc;
+        if (!fused) {
+            --n;
+            launch_attn(ap, d.kv_heads, st);
+            if ((rc = chk(hipGetLastError(), "attention"))) return rc;
+            // 4-wave workgroups for the o projection in the step (7B shape: +0.8-1.1%
+            // tokens/s over the 8 the standalone choice takes for 2048+ rows)
+            Cfg ocfg = choose_cfg(EPI_PLAIN, H, H / kQK, 1);
+            if (!g_force_waves) ocfg.waves = 4;
+            ocfg = dec_cfg(kDecO, ocfg);
+            if ((rc = chk(launch_gemv_epi(EPI_PLAIN, kFmtQ4, ocfg, p, 1, st), "o projection")))
+                return rc;
+        }
 
         // ffn RMSNorm + gate/up + SwiGLU
         p = make_params(kFmtQ4, L.gate, L.up, F, H, S->h1);
@@ -650,6 +775,7 @@ static int launch_step(arc_session* S, bool logits, uint32_t* nkernels)
         p.normw = L.ffn_norm;
         p.eps = d.rms_eps;
         p.y = S->s;
+        p.clear_done = S->done;  // the attention + o launch's done counter, for the next layer
         if ((rc = chk(launch_gemv_epi(EPI_SWIGLU, kFmtQ4, dec_cfg(kDecGateUp, choose_cfg(EPI_SWIGLU, F, H / kQK, 1)), p,
                                       1, st),
                       "gate/up")))
@@ -693,6 +819,13 @@ int arc_tune_decode(int kind, int bs, int rpl, int waves)
     for (const auto& c : ok) found = found || (c[0] == bs && c[1] == rpl);
     if (!found) return set_error(ARC_ERR_INVALID_ARGUMENT, "no kernel instance for bs=%d rpl=%d", bs, rpl);
     g_dec_cfg[kind] = Cfg{bs, bs ? rpl : 0, waves};
+    return ARC_OK;
+}
+
+int arc_tune_fuse_attn_o(int on)
+{
+    if (on != 0 && on != 1) return set_error(ARC_ERR_INVALID_ARGUMENT, "fuse_attn_o must be 0 or 1");
+    g_fuse_attn_o = on;
     return ARC_OK;
 }
 
@@ -974,6 +1107,7 @@ int arc_session_create(arc_model* m, uint32_t max_ctx, arc_session** out)
     plan.place(&S->best, size_t(S->best_cap) * sizeof(ArgBest));
     plan.place(&S->ctl, sizeof(DecodeCtl));
     plan.place(&S->counters, kCounters * sizeof(uint32_t));
+    plan.place(&S->done, kDoneCopies * kDoneStride * sizeof(uint32_t));
     plan.place(&S->out_tokens, size_t(S->out_cap) * sizeof(uint32_t));
     plan.place(&pf.h, size_t(kPfMaxM) * H * fl);
     plan.place(&pf.x, size_t(kPfMaxM) * H * sizeof(_Float16));
@@ -998,6 +1132,8 @@ int arc_session_create(arc_model* m, uint32_t max_ctx, arc_session** out)
     pf.host_tokens = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(S->pinned) + ctl_bytes + tok_bytes);
 
     if ((rc = check_hip(hipMemset(S->counters, 0, kCounters * sizeof(uint32_t)), "counters"))) return rc;
+    if ((rc = check_hip(hipMemset(S->done, 0, kDoneCopies * kDoneStride * sizeof(uint32_t)), "done counters")))
+        return rc;
     // rows past a prompt are read (never written) by the prompt-pass GEMM tiles
     if ((rc = check_hip(hipMemset(pf.x, 0, size_t(kPfMaxM) * H * sizeof(_Float16)), "prefill x"))) return rc;
     if ((rc = check_hip(hipMemset(pf.xs, 0, size_t(kPfMaxM) * d.ffn * sizeof(_Float16)), "prefill xs"))) return rc;
@@ -1106,7 +1242,7 @@ static int run_step(arc_session* s, bool logits, bool use_graph)
 // staging slot stays untouched until the call's final synchronisation.
 static int upload_ctl(arc_session* s, uint32_t i, uint32_t pos, uint32_t token)
 {
-    s->host_ctl[1 + i] = DecodeCtl{pos, token, 0u, 0u};
+    s->host_ctl[1 + i] = DecodeCtl{pos, token, 0u, 0u, 0u};
     return check_hip(hipMemcpyAsync(s->ctl, &s->host_ctl[1 + i], sizeof(DecodeCtl), hipMemcpyHostToDevice, s->stream),
                      "ctl upload");
 }
@@ -1118,6 +1254,9 @@ static int finish_call(arc_session* s, uint32_t* nonfinite, uint32_t* token)
                        "ctl download");
     if (rc) return rc;
     if ((rc = check_hip(hipStreamSynchronize(s->stream), "decode sync"))) return rc;
+    if (s->host_ctl[0].waits_expired)
+        return set_error(ARC_ERR_DEVICE, "%u cross-workgroup waits of the decode step gave up (results invalid)",
+                         s->host_ctl[0].waits_expired);
     if (nonfinite) *nonfinite = s->host_ctl[0].nonfinite;
     if (token) *token = s->host_ctl[0].token;
     return ARC_OK;
@@ -1248,7 +1387,7 @@ __global__ void k_attn_setup(uint32_t* counters, uint32_t n, DecodeCtl* ctl, uin
 {
     const uint32_t i = threadIdx.x;
     if (i < n) counters[i] = 0u;
-    if (i == 0) *ctl = DecodeCtl{pos, 0u, 0u, 0u};
+    if (i == 0) *ctl = DecodeCtl{pos, 0u, 0u, 0u, 0u};
 }
 
 struct AttnWorkspace {

@@ -38,6 +38,7 @@ struct DecodeCtl {
     uint32_t token;      // its id
     uint32_t step;       // tokens generated so far in this run
     uint32_t nonfinite;  // non-finite logits seen so far
+    uint32_t waits_expired;  // cross-workgroup waits that gave up (an error of the step)
 };
 struct ArgBest {
     float val;
@@ -255,6 +256,45 @@ __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t n, uint3
         const bool last = old + 1u == n;
         if (last) st_agent(counter, 0u);
         *flag = last ? 1u : 0u;
+    }
+    __syncthreads();
+    return *flag != 0u;
+}
+
+// A done counter one part of a launch raises and another part waits for is
+// held in kDoneCopies copies kDoneStride words (256 bytes) apart: each
+// waiting workgroup polls one copy, so no address takes more than a few
+// workgroups' polls (hundreds of workgroups polling one address queue up
+// behind each other, and behind the signal, for microseconds).
+constexpr int kDoneCopies = 64;
+constexpr int kDoneStride = 64;
+
+// Called by every thread of the workgroup after its st_agent stores: waits
+// until they have reached memory, then counts the workgroup in at each of
+// `copies` (<= 64) copies of a counter, `stride` words apart (one part of a
+// launch telling another that its results are readable; each waiter polls
+// one copy, so no single address takes every poll).
+__device__ __forceinline__ void signal_done(uint32_t* counter, uint32_t copies, uint32_t stride)
+{
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x < copies)
+        __hip_atomic_fetch_add(counter + threadIdx.x * stride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Called by every thread of the workgroup: waits until `counter` reaches n,
+// one thread polling with a short sleep between polls, at most kWaitPolls
+// polls (tens of milliseconds; a wait that long is an error the caller
+// reports).  Returns false when it gave up.  Only launches whose waiting
+// workgroups come after the ones they wait for in dispatch order, and fit on
+// the device together with them, wait at all.
+constexpr uint32_t kWaitPolls = 1u << 16;
+__device__ __forceinline__ bool wait_count(const uint32_t* counter, uint32_t n, uint32_t* flag)
+{
+    if (threadIdx.x == 0) {
+        uint32_t i = 0;
+        while (ld_agent(counter) < n && ++i < kWaitPolls) __builtin_amdgcn_s_sleep(2);
+        *flag = i < kWaitPolls ? 1u : 0u;
     }
     __syncthreads();
     return *flag != 0u;

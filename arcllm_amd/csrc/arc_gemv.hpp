@@ -98,7 +98,16 @@ struct GemvParams {
     uint32_t out_cap;
     uint32_t emb_rows;        // F_EMBED: rows of `emb` (a token id past them reads row 0)
     uint32_t ctx_rows;        // QKROPE/VSTORE: rows of the cache and RoPE table (positions clamped below)
+    uint32_t* clear_done;     // when set: the kDoneCopies copies of a done counter the previous launch
+                              // waited on, zeroed by workgroup 0 (that launch has ended)
 };
+
+// Zeroes the done-counter copies p.clear_done (workgroup 0 of the launch).
+__device__ __forceinline__ void clear_done_copies(const GemvParams& p)
+{
+    if (p.clear_done && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < unsigned(kDoneCopies))
+        p.clear_done[threadIdx.x * kDoneStride] = 0u;
+}
 
 // ------------------------------------------------------------ block loads
 // The header is read as the d/dmin dword and the 12 scale bytes separately:
@@ -826,15 +835,25 @@ constexpr int ring_depth()
 static_assert(ARC_PF_Q4 >= 2 && ARC_PF_Q6 >= 2 && ARC_PF_E148 >= 2, "a ring holds at least two buffers");
 
 // --------------------------------------------------------------- GEMV core
+// When x is ready: at the launch's start (NoXWait), or, in a launch whose
+// other part produces x, once a hook called by every thread of the
+// workgroup returns (kWaits).  A waiting GEMV issues its ring's first loads
+// before the wait and its x loads after it, with one more ring buffer, so
+// the weights are in flight while x is being produced.
+struct NoXWait {
+    static constexpr bool kWaits = false;
+    __device__ void operator()() const {}
+};
+
 // One workgroup's share of a GEMV launch: workgroup bx of gx (x dimension)
 // and split blockIdx.y.  k_gemv runs it over the whole grid; a fused launch
 // can give disjoint workgroup ranges to different GEMVs.
-template <int FMT, int BS, int RPL, int EPI, int W>
-__device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint32_t gx)
+template <int FMT, int BS, int RPL, int EPI, int W, class XWait = NoXWait>
+__device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint32_t gx, const XWait& xwait = XWait{})
 {
     static_assert(W == 4 || W == 8, "4 or 8 waves per workgroup");
     constexpr int NT = W * kWave;
-    constexpr int PF = ring_depth<FMT, EPI>();  // register buffers in the prefetch ring
+    constexpr int PF = ring_depth<FMT, EPI>() + (XWait::kWaits ? 1 : 0);  // register buffers in the prefetch ring
     // 16-byte aligned: the staged x is read as float4; the base follows the
     // kernel's static LDS, whose size is not a multiple of 16 in general
     extern __shared__ __align__(16) float lds[];
@@ -955,9 +974,13 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
             erow = p.emb + uint64_t(tok < p.emb_rows ? tok : 0u) * p.nb * kQ4Bytes;
         }
     XPre<NT> pre;
-    x_pre<FMT, NT>(pre, p.x, kb, nbl, rms, p.normw);
+    if constexpr (!XWait::kWaits) x_pre<FMT, NT>(pre, p.x, kb, nbl, rms, p.normw);
 #pragma unroll
     for (int u = 0; u < PF - 1; ++u) load_next(buf[u]);
+    if constexpr (XWait::kWaits) {
+        xwait();
+        x_pre<FMT, NT>(pre, p.x, kb, nbl, rms, p.normw);
+    }
 
     // Epilogue operands (bias, residual, accumulated output, RoPE factors) of
     // the tile being consumed, loaded at its first item ahead of that item's
@@ -1163,6 +1186,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p, uint32_t bx, uint
 template <int FMT, int BS, int RPL, int EPI, int W>
 __global__ __launch_bounds__(W * kWave) void k_gemv(GemvParams p)
 {
+    clear_done_copies(p);
     gemv_body<FMT, BS, RPL, EPI, W>(p, blockIdx.x, gridDim.x);
 }
 

@@ -299,6 +299,7 @@ __device__ __forceinline__ void gemv_rs_body(const GemvParams& p, uint32_t bx, u
 template <int NMAT, int RPL, int EPI, bool NORM, int W>
 __global__ __launch_bounds__(W * kWave) void k_gemv_rs(GemvParams p)
 {
+    clear_done_copies(p);
     gemv_rs_body<NMAT, RPL, EPI, NORM, W>(p, blockIdx.x, gridDim.x);
 }
 

@@ -1152,7 +1152,7 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
         if ((rc = check_hip(hipMemcpyAsync(pf->tokens, ht, M * sizeof(uint32_t), hipMemcpyHostToDevice, st), "tokens")))
             return rc;
         // the LM head of the last row leaves position p0 + M in the control block
-        S->host_ctl[1 + pass] = DecodeCtl{p0 + M - 1, 0u, 0u, 0u};
+        S->host_ctl[1 + pass] = DecodeCtl{p0 + M - 1, 0u, 0u, 0u, 0u};
         if ((rc = check_hip(hipMemcpyAsync(S->ctl, &S->host_ctl[1 + pass], sizeof(DecodeCtl), hipMemcpyHostToDevice, st),
                             "ctl upload")))
             return rc;

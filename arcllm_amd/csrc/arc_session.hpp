@@ -130,6 +130,7 @@ struct arc_session {
     float *h = nullptr, *h1 = nullptr, *q = nullptr, *attn = nullptr, *s = nullptr, *logits = nullptr;
     float *apo = nullptr, *apml = nullptr;  // attention split partials [kv_heads][kMaxSplits][hpk][...]
     uint32_t* counters = nullptr;            // kCounters arrival counters
+    uint32_t* done = nullptr;                // kDoneCopies copies of the attention + o done counter
     float2* rope = nullptr;  // [max_ctx][64] (cos, sin) of pos * theta^(-2p/128)
     arc::ArgBest* best = nullptr;
     uint32_t best_cap = 0;

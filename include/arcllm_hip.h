@@ -262,6 +262,10 @@ int arc_tune_attention(int waves, int min_chunks_per_split);
  * GEMV of decode steps captured later on this host thread: kind 0 the o
  * projection, 1 the fused gate/up, 2 the down projection, 3 the LM head. */
 int arc_tune_decode(int kind, int bs, int rpl, int waves);
+/* Tuning hook: 1 (default) runs each layer's attention and o projection of
+ * decode steps captured later on this host thread as one launch, whose o
+ * workgroups wait (bounded) for the attention's output; 0 as two launches. */
+int arc_tune_fuse_attn_o(int on);
 
 /* Diagnostic: streaming read of `bytes` (16-byte aligned) with `grid`
  * workgroups of 256 lanes, 16 bytes per lane access, xor-folded into

@@ -47,6 +47,7 @@ class Config:
     kv_dim: int = 0               # QKROPE / VSTORE cache row width
     pos: int = 0
     max_ctx: int = 1
+    ring: int = RING              # register buffers (a GEMV that waits for its x takes one more)
 
 
 @dataclass
@@ -201,7 +202,7 @@ def simulate(c: Config, mistake: str | None = None) -> Report:
 
                 # the ring: PF-1 loads before the first item, one per item;
                 # load k reads item min(k, S-1) (item 0 when S = 0)
-                for k in range(RING - 1 + S):
+                for k in range(c.ring - 1 + S):
                     it = min(k, S - 1) if S > 0 else 0
                     load(it // nj, it % nj)
 

@@ -173,6 +173,48 @@ def test_seven_query_heads_per_kv_head_long_context():
             assert_tokens_match(gpu, ref_t, second, margins, scale)
 
 
+def test_attention_o_one_launch_matches_two_launches():
+    """Attention and the o projection as one launch (the o workgroups load
+    their first weights, then wait for every kv head's output) against the
+    two-launch step, on the 7-heads-per-kv-head grouping at a one-split and
+    a many-split context, captured graph and eager: first-step logits within
+    1e-5 of the logit scale (the two o launches may sum in another lane
+    layout), the same 24 greedy tokens, 4 against 5 launches per layer, and
+    the same tokens again (the done and pass counters are back at zero)."""
+    d = arc.ModelDims()
+    d.hidden, d.q_heads, d.kv_heads, d.head_dim = 1792, 14, 2, 128
+    d.ffn, d.vocab, d.layers = 512, 2048, 2
+    d.rms_eps, d.rope_theta = 1e-6, 1e6
+    for layer in range(d.layers):
+        d.v_type[layer], d.down_type[layer] = arc.Q6_K, arc.Q4_K
+    T = arc.synth_model_tensors(d, SEED + 9)
+    model = arc.Model(d, T)
+    for ctx in (40, 700):
+        for graph in (True, False):
+            res = {}
+            for fuse in (True, False, True):
+                arc.tune_fuse_attn_o(fuse)
+                try:
+                    s = arc.Session(model, 760)
+                    s.fill_kv(ctx, 21)
+                    tok, nf0 = s.decode(5, ctx, 1, logits=True, graph=graph)
+                    lg = s.logits()
+                    toks, nf1 = s.decode(int(tok[0]), ctx + 1, 24, graph=graph)
+                    kps = s.kernels_per_step
+                finally:
+                    arc.tune_fuse_attn_o(True)
+                assert nf0 == 0 and nf1 == 0
+                assert kps == 1 + (4 if fuse else 5) * d.layers
+                if fuse in res:
+                    assert np.array_equal(lg, res[fuse][0]) and np.array_equal(toks, res[fuse][1])
+                res[fuse] = (lg, toks)
+            (lf, tf), (lu, tu) = res[True], res[False]
+            err = float(np.max(np.abs(lf.astype(np.float64) - lu))) / float(np.max(np.abs(lu)))
+            _log(f"ctx {ctx} graph {graph}: fused vs two launches, logits {err:.3g}, tokens {tf.tolist()}")
+            assert err <= 1e-5
+            assert np.array_equal(tf, tu)
+
+
 def test_decode_rejects_bad_requests():
     d = tiny_dims(layers=1)
     model = arc.Model(d, seed=3)
@@ -247,7 +289,7 @@ def test_qwen7b_shape_64_greedy_steps_match_oracle(qwen7b_fixture, ctx):
     _log(f"ctx {ctx}: gpu {gpu.tolist()}\n         oracle {ref.tolist()}\n         min margin {margins.min():.4g} "
          f"(bound {TIE_BOUND} * max|logit|), kernels/step {sess.kernels_per_step}")
     assert nf0 == 0 and nf1 == 0
-    assert sess.kernels_per_step == 1 + 5 * d.layers  # 5 per layer, LM head + argmax
+    assert sess.kernels_per_step == 1 + 4 * d.layers  # 4 per layer (attention + o fused), LM head + argmax
     matched = assert_tokens_match(gpu, ref, second, margins, scales)
     _log(f"ctx {ctx}: {matched} of {steps} steps compared and identical")
     # the kernels are deterministic and the fixture fixed: every one of the

@@ -85,6 +85,17 @@ def test_qkrope_and_vstore_epilogues_stay_in_bounds():
             assert not r.violations, (gx, r.violations)
 
 
+def test_attention_o_launch_gemv_part_stays_in_bounds():
+    """The o projection's part of the attention + o launch: Q4_K, 8 quads
+    per row, one row per lane, 4 waves, a ring of 3 buffers (the loads of
+    two items go out before the wait for x), over one workgroup to one wave
+    tile per wave, at the 7B shape and small ones."""
+    for rows in (256, 1792, 3584):
+        c = gb.Config(gb.Q4, 8, 1, gb.PLAIN, 4, rows, rows, ring=3)
+        for gx, r in run(c):
+            assert not r.violations, (rows, gx, r.violations)
+
+
 @pytest.mark.parametrize("mistake", ["row", "block"])
 def test_planted_index_mistake_is_reported(mistake):
     found = False

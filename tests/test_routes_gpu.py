@@ -65,7 +65,7 @@ def test_session_route_down_switches_and_matches_oracle():
         s.fill_kv(ctx, kv_seed)
         toks, nf = s.decode(77, ctx, steps)
         assert nf == 0
-        assert s.kernels_per_step == 1 + 5 * d.layers
+        assert s.kernels_per_step == 1 + 4 * d.layers
         results[name] = toks
         _log(f"route {name}: {toks.tolist()}")
         o.fill_kv(ctx, kv_seed, arc.synth_normal)
