@@ -91,6 +91,7 @@ _SIGS = {
     "arc_tune_attention": [C.c_int, C.c_int],
     "arc_tune_decode": [C.c_int, C.c_int, C.c_int, C.c_int],
     "arc_tune_fuse_attn_o": [C.c_int],
+    "arc_tune_prefill_attention": [C.c_int],
     "arc_probe_read": [_P, C.c_size_t, _P, _U32, _P],
     "arc_probe_read_unrolled": [_P, C.c_size_t, _P, _U32, C.c_int, _P],
     "arc_exec148_materialize": [_P, _U32, _U32, _P, _P],
@@ -477,6 +478,11 @@ def tune_attention(waves: int = 0, min_chunks_per_split: int = 0) -> None:
     """Decode attention launch shape: waves per workgroup (4 or 8) and the
     least chunks of 16 * waves positions per split; 0 = automatic."""
     check(lib().arc_tune_attention(int(waves), int(min_chunks_per_split)))
+
+
+def tune_prefill_attention(mfma: bool = True) -> None:
+    """The prompt pass's attention kernel: MFMA (default) or VALU."""
+    check(lib().arc_tune_prefill_attention(1 if mfma else 0))
 
 
 def tune_fuse_attn_o(on: bool = True) -> None:

@@ -974,10 +974,221 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float* __restrict__ q, co
     }
 }
 
+// Causal GQA of the prompt pass on MFMA.  Workgroup (query block b of 32
+// rows, q head hq of kv head hq / hpk): 4 waves; wave w takes the
+// 64-position key chunks w, w + 4, ... of positions 0 .. the block's last,
+// with its own online softmax per query; at the end the waves' states are
+// combined through LDS in wave order.
+//  scores  S^T = K Q^T per 32-key tile on v_mfma_f32_32x32x16_f16: A = K
+//          rows straight from the cache (lane -> key lane%32; step s: dims
+//          16s + 8(lane/32) .. +7, 16 bytes of the row), B = Q^T (lane ->
+//          query lane%32, the same dims) as fp16 hi + lo parts (q = hi + lo
+//          to 2^-22 relative; K*hi and K*lo are exact products).  D: lane ->
+//          query lane%32, value i -> key 8(i/4) + 4(lane/32) + i%4.
+//  softmax the chunk maximum of a query from the lane's 32 scores and its
+//          partner half-wave's (lane ^ 32); positions past the query's own
+//          are masked.  Weights e^(x - max), rescaling the running sum and
+//          the output by e^(max_old - max_new).
+//  values  O^T = V^T P^T: B = P^T straight from the lane's weights (step s of
+//          a tile: values 8s .. 8s+7, keys 16s + 8(j/4) + 4(lane/32) + j%4)
+//          as fp16 hi + lo; A = V^T from LDS, where the wave stages its chunk
+//          transposed with key k at column k with bits 2 and 3 swapped, so a
+//          lane's 8 keys of a step are 16 contiguous bytes.  D: lane ->
+//          query lane%32, value i of dim tile t -> dim 32t + 8(i/4) +
+//          4(lane/32) + i%4.
+// Semantics as k_pf_attn (src/arcllm_v1_runtime.cpp:340-369 per row).
+constexpr int kVtLd = kChunk + 8;  // halves per V^T row in LDS (padded)
+
+__device__ __forceinline__ uint32_t swap_bits_2_3(uint32_t k)
+{
+    return (k & ~12u) | ((k & 4u) << 1) | ((k & 8u) >> 1);
+}
+
+__global__ __launch_bounds__(256, 2) void k_pf_attn_mf(const float* __restrict__ q, const _Float16* __restrict__ kc,
+                                                       const _Float16* __restrict__ vc, uint32_t kv_heads,
+                                                       uint32_t hpk, uint32_t pos0, uint32_t M, uint32_t max_ctx,
+                                                       float scale, _Float16* __restrict__ x, uint32_t ldx)
+{
+    __shared__ __align__(16) _Float16 vt[4][kHeadDim][kVtLd];  // per wave: its chunk's V^T; then the outputs
+    __shared__ float mw[4][32], lw[4][32];
+    const uint32_t b = blockIdx.x, hq = blockIdx.y, g = hq / hpk;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l32 = lane & 31, h2 = lane >> 5;
+    const uint32_t kvd = kv_heads * kHeadDim, hidden = kv_heads * hpk * kHeadDim;
+    const uint32_t q0 = b * 32, qlast = min(q0 + 31, M - 1);
+    const uint32_t qpos = pos0 + q0 + uint32_t(l32);  // this lane's query position
+    const uint32_t nkc = (pos0 + qlast + kChunk) / kChunk;  // chunks holding positions 0 .. pos0 + qlast
+
+    half8 qh[8], ql[8];  // B operand of the scores: query l32, dims 16s + 8 h2 .. +7
+    {
+        const float* qp = q + uint64_t(min(q0 + uint32_t(l32), M - 1)) * hidden + hq * kHeadDim + 8 * h2;
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+            const float4 a = *reinterpret_cast<const float4*>(qp + 16 * st);
+            const float4 c = *reinterpret_cast<const float4*>(qp + 16 * st + 4);
+            const float f[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const _Float16 hi = static_cast<_Float16>(f[j]);
+                qh[st][j] = hi;
+                ql[st][j] = static_cast<_Float16>(f[j] - static_cast<float>(hi));
+            }
+        }
+    }
+    f32x16 o[4];  // O^T: dim tile t, query l32
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[t][i] = 0.0f;
+    float mrun = -INFINITY, lrun = 0.0f;  // lrun: this half-wave's share
+    _Float16(*vw)[kVtLd] = vt[w];
+
+    for (uint32_t c = uint32_t(w); c < nkc; c += 4) {
+        const uint32_t kbase = c * kChunk;
+        // this chunk's V rows (lane -> key kbase + lane), 16 bytes at a time,
+        // and both tiles' K fragments, all issued before any is used
+        uint4 vr[16];
+        {
+            const uint4* vp = reinterpret_cast<const uint4*>(vc + uint64_t(min(kbase + uint32_t(lane), max_ctx - 1)) * kvd +
+                                                             g * kHeadDim);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) vr[e] = vp[e];
+        }
+        uint4 kf[2][8];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const uint4* kp = reinterpret_cast<const uint4*>(
+                kc + uint64_t(min(kbase + 32u * kt + uint32_t(l32), max_ctx - 1)) * kvd + g * kHeadDim + 8 * h2);
+#pragma unroll
+            for (int st = 0; st < 8; ++st) kf[kt][st] = kp[2 * st];
+        }
+        // scores of the two 32-key tiles
+        f32x16 sc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sc[kt][i] = 0.0f;
+#pragma unroll
+            for (int st = 0; st < 8; ++st) {
+                const half8 kfr = __builtin_bit_cast(half8, kf[kt][st]);
+                sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kfr, qh[st], sc[kt], 0, 0, 0);
+                sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kfr, ql[st], sc[kt], 0, 0, 0);
+            }
+        }
+        // V^T of the chunk into the wave's LDS rows (key k -> column swap_bits_2_3(k))
+        {
+            const uint32_t col = swap_bits_2_3(uint32_t(lane));
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const half8 v8 = __builtin_bit_cast(half8, vr[e]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) vw[8 * e + j][col] = v8[j];
+            }
+        }
+        // masked, scaled scores; the chunk maximum per query
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t kpos = kbase + 32u * kt + 8u * (i >> 2) + 4u * h2 + (i & 3);
+                const float v = kpos <= qpos ? sc[kt][i] * scale : -INFINITY;
+                sc[kt][i] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = xor_max<32>(mx);
+        const float mnew = fmaxf(mrun, mx);
+        const float mr = mnew == -INFINITY ? 0.0f : mnew;  // no position <= the query's yet: all weights 0
+        const float alpha = expf(mrun - mr);              // mrun = -inf: 0
+        float es = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float e = expf(sc[kt][i] - mr);
+                sc[kt][i] = e;
+                es += e;
+            }
+        lrun = lrun * alpha + es;
+        mrun = mnew;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[t][i] *= alpha;
+        // the wave's own V^T rows: its LDS writes above complete before these reads
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                half8 ph, pl;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float pv = sc[kt][8 * st + j];
+                    const _Float16 hi = static_cast<_Float16>(pv);
+                    ph[j] = hi;
+                    pl[j] = static_cast<_Float16>(pv - static_cast<float>(hi));
+                }
+                const uint32_t k0 = 32u * kt + 16u * st + 8u * h2;  // the lane's 8 keys, contiguous in LDS
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const half8 va = *reinterpret_cast<const half8*>(&vw[32 * t + l32][k0]);
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph, o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl, o[t], 0, 0, 0);
+                }
+            }
+        // the next chunk's V^T overwrites these rows
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    // the waves' states, combined in wave order: M = max m_w, f_w = e^(m_w - M),
+    // out = sum_w f_w o_w / sum_w f_w l_w (waves without a chunk: m = -inf, f = 0)
+    const float ltot = xor_sum<32>(lrun);
+    __syncthreads();  // every wave is done with its V^T rows
+    float* ot = reinterpret_cast<float*>(&vt[0][0][0]);  // [4][128 dims][32 queries]
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t d = 32u * t + 8u * (i >> 2) + 4u * h2 + (i & 3);
+            ot[(w * kHeadDim + d) * 32 + l32] = o[t][i];
+        }
+    if (h2 == 0) {
+        mw[w][l32] = mrun;
+        lw[w][l32] = ltot;
+    }
+    __syncthreads();
+    const uint32_t qq = uint32_t(tid) & 31u, d0 = (uint32_t(tid) >> 5) * 16u;
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) Mx = fmaxf(Mx, mw[v][qq]);  // finite: chunk 0 holds position 0 <= every query's
+    float f[4], L = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        f[v] = expf(mw[v][qq] - Mx);
+        L = __builtin_fmaf(lw[v][qq], f[v], L);
+    }
+    const float li = 1.0f / L;
+    if (q0 + qq < M) {
+        _Float16* dst = x + uint64_t(q0 + qq) * ldx + hq * kHeadDim + d0;
+#pragma unroll
+        for (int d = 0; d < 16; ++d) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc = __builtin_fmaf(ot[(v * kHeadDim + d0 + d) * 32 + qq], f[v], acc);
+            dst[d] = _Float16(acc * li);
+        }
+    }
+}
+
 // ------------------------------------------------------------------ host
 namespace {
 
 constexpr uint32_t kPfTargetWgs = 256;
+thread_local int g_pf_attn_mfma = 1;  // 0: the VALU attention kernel (k_pf_attn)
 
 template <int FMT, int MB, int NF, bool SW>
 hipError_t launch_gemm_t(const PfGemm& p, uint32_t gx, uint32_t splits, hipStream_t st)
@@ -1198,7 +1409,11 @@ int run_prefill(arc_session* S, const uint32_t* tokens, uint32_t n, uint32_t pos
                                uint32_t(kPfMaxM), H, kvd, L.qb, L.kb, L.vb, S->rope, p0, pf->q, kc, vc);
             if ((rc = chk(hipGetLastError(), "q/k/v epilogue"))) return rc;
             // attention -> x
-            launch_attn(hpk, dim3(M, d.kv_heads), st, pf->q, kc, vc, d.kv_heads, p0, scale, pf->x, H);
+            if (g_pf_attn_mfma)
+                hipLaunchKernelGGL(k_pf_attn_mf, dim3((M + 31) / 32, d.q_heads), dim3(256), 0, st, pf->q, kc, vc,
+                                   d.kv_heads, hpk, p0, M, S->max_ctx, scale, pf->x, H);
+            else
+                launch_attn(hpk, dim3(M, d.kv_heads), st, pf->q, kc, vc, d.kv_heads, p0, scale, pf->x, H);
             if ((rc = chk(hipGetLastError(), "prefill attention"))) return rc;
             // o + residual + ffn norm
             g.w0 = g.w1 = L.o;
@@ -1319,6 +1534,13 @@ int pf_reduce(const float* part, uint32_t splits, uint32_t M, uint32_t N, float*
 using namespace arc;
 
 extern "C" {
+
+int arc_tune_prefill_attention(int mfma)
+{
+    if (mfma != 0 && mfma != 1) return set_error(ARC_ERR_INVALID_ARGUMENT, "prefill attention: 0 (VALU) or 1 (MFMA)");
+    g_pf_attn_mfma = mfma;
+    return ARC_OK;
+}
 
 size_t arc_prefill_gemm_workspace_bytes(uint32_t N, uint32_t K)
 {

@@ -262,6 +262,11 @@ int arc_tune_attention(int waves, int min_chunks_per_split);
  * GEMV of decode steps captured later on this host thread: kind 0 the o
  * projection, 1 the fused gate/up, 2 the down projection, 3 the LM head. */
 int arc_tune_decode(int kind, int bs, int rpl, int waves);
+/* Tuning hook: the prompt pass's attention kernel for passes run later on
+ * this host thread: 1 (default) on MFMA (query blocks of 32 rows per q
+ * head, key chunks over 4 waves), 0 the VALU kernel (one query row per
+ * workgroup and kv head). */
+int arc_tune_prefill_attention(int mfma);
 /* Tuning hook: 1 (default) runs each layer's attention and o projection of
  * decode steps captured later on this host thread as one launch, whose o
  * workgroups wait (bounded) for the attention's output; 0 as two launches. */

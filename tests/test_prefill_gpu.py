@@ -113,6 +113,42 @@ def test_mfma_prefill_matches_oracle(n):
     assert s.prefill_kernels == 8 * d.layers + 3
 
 
+@pytest.mark.parametrize("n", [37, 300])
+def test_prefill_attention_mfma_matches_valu_kernel(n):
+    """The prompt pass's attention on MFMA (32-row query blocks per q head,
+    key chunks over 4 waves merged in LDS) against the VALU kernel (one
+    query row per workgroup), on the 7-q-heads-per-kv-head grouping, one
+    pass (37 tokens) and two passes (300: the second starts at position
+    256): last-position logits and every layer's cache rows within 2e-3
+    normwise, the same next token."""
+    d = arc.ModelDims()
+    d.hidden, d.q_heads, d.kv_heads, d.head_dim = 1792, 14, 2, 128
+    d.ffn, d.vocab, d.layers = 512, 2048, 3
+    d.rms_eps, d.rope_theta = 1e-6, 1e6
+    for layer in range(d.layers):
+        d.v_type[layer], d.down_type[layer] = arc.Q6_K, arc.Q4_K
+    T = arc.synth_model_tensors(d, SEED + 11)
+    model = arc.Model(d, T)
+    prompt = np.random.default_rng(11).integers(0, d.vocab, n).astype(np.uint32)
+    res = {}
+    for mfma in (True, False):
+        arc.tune_prefill_attention(mfma)
+        try:
+            sess = arc.Session(model, 320)
+            nxt, _ = sess.prefill(prompt, logits=True)
+            lg = sess.logits()
+            caches = [_cache(sess, d, layer, n, 320) for layer in range(d.layers)]
+        finally:
+            arc.tune_prefill_attention(True)
+        res[mfma] = (int(nxt), lg, caches)
+    (n1, l1, c1), (n0, l0, c0) = res[True], res[False]
+    e = norm_err(l1, l0)
+    ec = max(norm_err(a, b) for la, lb in zip(c1, c0) for a, b in zip(la, lb))
+    _log(f"n {n}: mfma vs valu attention: logits {e:.3g}, caches {ec:.3g}, next {n1} / {n0}")
+    assert e <= 2e-3 and ec <= 2e-3
+    assert n1 == n0
+
+
 def test_mfma_prefill_two_passes_and_offset():
     d = tiny_dims(layers=2)
     T = arc.synth_model_tensors(d, SEED + 7)
