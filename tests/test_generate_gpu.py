@@ -79,7 +79,7 @@ def test_generate_cli_matches_oracle(tmp_path):
     assert len(gpu) == max_new
     _log(f"near-tie steps: {oracle_follow(d, T, prompt, gpu)}")
     st = res["stats"]
-    per_step = 1 + 5 * d.layers
+    per_step = 1 + 4 * d.layers  # q/k/v, attention + o, gate/up, down; LM head + next token
     # batched prompt pass: embed + first norm, 8 launches per layer, LM head + next token
     assert st["prefill_dispatches"] == 8 * d.layers + 3 and st["prefill_submits"] == 1
     assert st["decode_dispatches_per_step"] == per_step and st["decode_submits_per_step"] == 1
