@@ -103,6 +103,7 @@ _SIGS = {
     "arc_prefill_gemm": [C.c_int, _P, _U32, _U32, _P, _U32, _P, _P, _P],
     "arc_prefill_gateup": [_P, _P, _U32, _U32, _P, _U32, _P, _P, _P],
     "arc_prefill_qkv": [_P, _P, _P, C.c_int, _U32, _U32, _U32, _P, _U32, _P, _P, _P],
+    "arc_prefill_attention": [_P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _U32, C.c_int, _P],
 }
 _RESTYPE = {
     "arc_last_error": C.c_char_p,
@@ -455,6 +456,14 @@ def prefill_gateup(w_gate, w_up, N: int, K: int, x, M: int, s, workspace, stream
     """The prompt pass's fused gate/up + SwiGLU: s[M][N] (fp16)."""
     check(lib().arc_prefill_gateup(_ptr(w_gate), _ptr(w_up), N, K, _ptr(x), M, _ptr(s), _ptr(workspace),
                                    _sp(stream)))
+
+
+def prefill_attention(q, kc, vc, kv_heads: int, hpk: int, max_ctx: int, pos0: int, M: int, x, ldx: int,
+                      mfma: bool = True, stream: Optional[Stream] = None) -> None:
+    """The prompt pass's causal GQA: x[m] (fp16, row stride ldx) for prompt rows m < M at positions
+    pos0 + m over the fp16 caches; MFMA kernel (default) or the VALU one."""
+    check(lib().arc_prefill_attention(_ptr(q), _ptr(kc), _ptr(vc), kv_heads, hpk, max_ctx, pos0, M, _ptr(x), ldx,
+                                      1 if mfma else 0, _sp(stream)))
 
 
 def prefill_qkv(wq, wk, wv, v_qtype: int, H: int, kvd: int, K: int, x, M: int, y, workspace,

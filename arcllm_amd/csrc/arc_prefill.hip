@@ -1610,6 +1610,35 @@ int arc_prefill_gateup(const void* w_gate, const void* w_up, uint32_t N, uint32_
     return check_hip(launch_gateup(u, m_blocks(M), (N + 127) / 128, st), "prompt-pass gate/up");
 }
 
+int arc_prefill_attention(const float* q, const void* kc, const void* vc, uint32_t kv_heads, uint32_t hpk,
+                          uint32_t max_ctx, uint32_t pos0, uint32_t M, uint16_t* x, uint32_t ldx, int mfma,
+                          arc_stream_t stream)
+{
+    if (!q || !kc || !vc || !x) return set_error(ARC_ERR_INVALID_ARGUMENT, "null argument");
+    if (kv_heads == 0 || kv_heads > 64 || hpk == 0 || hpk > uint32_t(kMaxHpk))
+        return set_error(ARC_ERR_UNSUPPORTED, "prefill attention supports 1..64 kv heads and 1..%d query heads per kv "
+                         "head", kMaxHpk);
+    if (M == 0 || max_ctx == 0 || max_ctx > uint32_t(kMaxChunks * kChunk) || uint64_t(pos0) + M > max_ctx)
+        return set_error(ARC_ERR_INVALID_ARGUMENT, "bad rows: pos0 %u + M %u > max_ctx %u (at most %d)", pos0, M,
+                         max_ctx, kMaxChunks * kChunk);
+    const uint32_t hidden = kv_heads * hpk * kHeadDim;
+    if (ldx < hidden) return set_error(ARC_ERR_INVALID_ARGUMENT, "ldx %u < %u", ldx, hidden);
+    const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) |
+                         reinterpret_cast<uintptr_t>(vc);
+    if (al & 15u) return set_error(ARC_ERR_INVALID_ARGUMENT, "q, kc and vc must be 16-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const _Float16* k16 = static_cast<const _Float16*>(kc);
+    const _Float16* v16 = static_cast<const _Float16*>(vc);
+    _Float16* x16 = reinterpret_cast<_Float16*>(x);
+    const float scale = 1.0f / std::sqrt(float(kHeadDim));
+    if (mfma)
+        hipLaunchKernelGGL(k_pf_attn_mf, dim3((M + 31) / 32, kv_heads * hpk), dim3(256), 0, st, q, k16, v16, kv_heads,
+                           hpk, pos0, M, max_ctx, scale, x16, ldx);
+    else
+        launch_attn(hpk, dim3(M, kv_heads), st, q, k16, v16, kv_heads, pos0, scale, x16, ldx);
+    return check_hip(hipGetLastError(), "prefill attention");
+}
+
 int arc_prefill_qkv(const void* wq, const void* wk, const void* wv, int v_qtype, uint32_t H, uint32_t kvd, uint32_t K,
                     const uint16_t* x, uint32_t M, float* y, void* workspace, arc_stream_t stream)
 {

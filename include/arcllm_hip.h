@@ -241,6 +241,18 @@ int arc_prefill_gateup(const void *w_gate, const void *w_up, uint32_t N, uint32_
 int arc_prefill_qkv(const void *wq, const void *wk, const void *wv, int v_qtype, uint32_t H, uint32_t kvd, uint32_t K,
                     const uint16_t *x, uint32_t M, float *y, void *workspace, arc_stream_t stream);
 
+/* The prompt pass's causal GQA, with its kernel: prompt row m (position
+ * pos0 + m, m < M) attends to cache positions 0 .. pos0 + m.  q: fp32
+ * [M][kv_heads * hpk * 128] (RoPE applied); kc, vc: fp16 bits
+ * [max_ctx][kv_heads * 128], rows 0 .. pos0 + M - 1 written; x: fp16 bits,
+ * row m at x + m * ldx (ldx >= kv_heads * hpk * 128).  mfma = 1: the MFMA
+ * kernel the prompt pass runs, 0: the VALU kernel.  Replaces the per-row
+ * attention of build_prefill (src/arcllm_v1_runtime.cpp:340-369, with the
+ * semantics of src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1177-1212). */
+int arc_prefill_attention(const float *q, const void *kc, const void *vc, uint32_t kv_heads, uint32_t hpk,
+                          uint32_t max_ctx, uint32_t pos0, uint32_t M, uint16_t *x, uint32_t ldx, int mfma,
+                          arc_stream_t stream);
+
 /* Tuning hook: force the GEMV lane layout for later launches on this host
  * thread (bs = super-block quads per row: 1,2,4,8,16; rpl = rows per lane:
  * 1,2,4).  bs = 0 restores the automatic choice. */

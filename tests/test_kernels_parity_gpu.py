@@ -9,6 +9,10 @@ src/arcllm_v1_i001r_p8c_profile_runtime.cpp:1177-1212
 context lengths on both sides of every chunk and split boundary, 7 query
 heads per kv head (the 7B shape).
 
+Prompt-pass attention (arc_prefill_attention: the MFMA kernel the pass runs
+and the VALU one), row by row against the same fp64 attention over positions
+0 .. pos0 + m.
+
 Prompt pass (arc_prefill_gemm / arc_prefill_gateup / arc_prefill_qkv: the
 run_prefill kernels, split plans and fixed-order split reductions):
 oracle orc_gemv_r64_f16 (each decoded weight and each input element rounded
@@ -213,3 +217,42 @@ def test_prefill_gemm_rejects_bad_arguments():
         arc.prefill_gemm(arc.Q6_K, w, 512, H, x, 4, y, ws)  # GGUF Q6_K: the prompt pass reads it padded
     with pytest.raises(arc.ArcError):
         arc.prefill_gemm(arc.Q4_K, w, 512, 1000, x, 4, y, ws)  # K not a multiple of 256
+
+
+# ------------------------------------------------ prompt-pass attention
+@pytest.mark.parametrize("mfma", [True, False])
+@pytest.mark.parametrize("pos0,M,qscale", [(0, 37, 1.0), (0, 256, 1.0), (0, 256, 4.0), (256, 44, 1.0),
+                                            (1000, 64, 4.0), (3900, 256, 1.0)])
+def test_prefill_attention_vs_fp64(kv_cache, mfma, pos0, M, qscale):
+    """The prompt pass's causal GQA (7 q heads per kv head), MFMA and VALU
+    kernels: prompt row m at position pos0 + m against the fp64 attention
+    over positions 0 .. pos0 + m (the decode oracle), per element within
+    1e-3, on rows covering the 32-row query blocks' edges and, with pos0 >
+    0, the offset passes of long prompts.  The output is fp16: its rounding
+    (<= 2^-11 relative) is inside the bar."""
+    max_ctx, kc, vc, dkc, dvc = kv_cache
+    hidden = KVH * HPK * 128
+    q = (arc.synth_normal(SEED, 300 + pos0 + M, M * hidden) * qscale).astype(np.float32)
+    x = arc.DeviceBuffer(M * hidden * 2)
+    arc.prefill_attention(dev(q), dkc, dvc, KVH, HPK, max_ctx, pos0, M, x, hidden, mfma=mfma)
+    got = x.download(np.uint16, M * hidden).view(np.float16).astype(np.float64).reshape(M, hidden)
+    worst = 0.0
+    for m in [r for r in check_rows(M) if r < M] + [M - 1]:
+        ref = orc.attention_decode_f64(q[m * hidden:(m + 1) * hidden], kc, vc, pos0 + m + 1, KVH * HPK, KVH)
+        worst = max(worst, orc.rel_err(got[m], ref))
+    print(f"prefill attention mfma={mfma} pos0={pos0} M={M} qscale={qscale}: per-element error {worst:.3g}",
+          flush=True)
+    assert worst <= TOL
+
+
+def test_prefill_attention_rejects_bad_arguments(kv_cache):
+    max_ctx, kc, vc, dkc, dvc = kv_cache
+    hidden = KVH * HPK * 128
+    q = arc.DeviceBuffer(4 * hidden * 4)
+    x = arc.DeviceBuffer(4 * hidden * 2)
+    with pytest.raises(arc.ArcError):
+        arc.prefill_attention(q, dkc, dvc, KVH, HPK, max_ctx, max_ctx - 2, 4, x, hidden)  # rows past the cache
+    with pytest.raises(arc.ArcError):
+        arc.prefill_attention(q, dkc, dvc, KVH, 9, max_ctx, 0, 4, x, hidden)  # 9 q heads per kv head
+    with pytest.raises(arc.ArcError):
+        arc.prefill_attention(q, dkc, dvc, KVH, HPK, max_ctx, 0, 4, x, hidden - 8)  # ldx below the row
