@@ -494,10 +494,11 @@ def tune_prefill_attention(mfma: bool = True) -> None:
     check(lib().arc_tune_prefill_attention(1 if mfma else 0))
 
 
-def tune_fuse_attn_o(on: bool = True) -> None:
+def tune_fuse_attn_o(on=True) -> None:
     """Attention and o projection of decode steps captured later as one
-    launch (default) or two."""
-    check(lib().arc_tune_fuse_attn_o(1 if on else 0))
+    launch (default) or two; 2 = one launch whose attention withholds its
+    signal (a test of the bounded wait: the decode call then fails)."""
+    check(lib().arc_tune_fuse_attn_o(int(on) if not isinstance(on, bool) else (1 if on else 0)))
 
 
 DEC_O, DEC_GATEUP, DEC_DOWN, DEC_LMHEAD = 0, 1, 2, 3

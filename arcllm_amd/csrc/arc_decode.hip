@@ -45,6 +45,7 @@ struct AttnParams {
     float scale;
     uint32_t* done;           // in the launch fused with the o projection: kDoneCopies copies of a
                               // counter raised once per kv head when its output is written (past the L2)
+    uint32_t withhold;        // test of the bounded wait: nonzero = the attention never raises `done`
 };
 
 // Split plan of one decode position over T cached positions: chunks of
@@ -299,7 +300,8 @@ __device__ __forceinline__ void attn_body(const AttnParams& a, const uint32_t s,
             const float li = 1.0f / Lsp;
             store_out(make_float4(osp.x * li, osp.y * li, osp.z * li, osp.w * li));
         }
-        if constexpr (FUSED) signal_done(a.done, kDoneCopies, kDoneStride);
+        if constexpr (FUSED)
+            if (!a.withhold) signal_done(a.done, kDoneCopies, kDoneStride);
         return;
     }
     // this split's partials, written past the L2 for the merging workgroup
@@ -387,7 +389,8 @@ __device__ __forceinline__ void attn_body(const AttnParams& a, const uint32_t s,
         }
         store_out(r);
     }
-    if constexpr (FUSED) signal_done(a.done, kDoneCopies, kDoneStride);
+    if constexpr (FUSED)
+        if (!a.withhold) signal_done(a.done, kDoneCopies, kDoneStride);
 }
 
 template <int HPK, int W>
@@ -496,7 +499,7 @@ static void launch_attn(AttnParams ap, uint32_t kv_heads, hipStream_t st)
 
 // Attention + o projection in one launch (k_attn_o): 1 automatic, 0 two
 // launches (tuning and comparison).
-inline thread_local int g_fuse_attn_o = 1;
+inline thread_local int g_fuse_attn_o = 1;  // 2: fused, the attention withholding its signal (test)
 
 template <int HPK>
 static hipError_t launch_attn_o_hpk(const AttnParams& ap, GemvParams o, hipStream_t st, bool* done)
@@ -538,6 +541,7 @@ static hipError_t launch_attn_o(AttnParams ap, const GemvParams& o, hipStream_t 
         g_dec_cfg[kDecO].bs || g_dec_cfg[kDecO].waves)
         return hipSuccess;
     ap.min_cps = g_attn_min_cps > 0 ? uint32_t(g_attn_min_cps) : 1u;
+    ap.withhold = g_fuse_attn_o == 2 ? 1u : 0u;
     switch (ap.hpk) {
     case 1: return launch_attn_o_hpk<1>(ap, o, st, done);
     case 2: return launch_attn_o_hpk<2>(ap, o, st, done);
@@ -824,7 +828,7 @@ int arc_tune_decode(int kind, int bs, int rpl, int waves)
 
 int arc_tune_fuse_attn_o(int on)
 {
-    if (on != 0 && on != 1) return set_error(ARC_ERR_INVALID_ARGUMENT, "fuse_attn_o must be 0 or 1");
+    if (on < 0 || on > 2) return set_error(ARC_ERR_INVALID_ARGUMENT, "fuse_attn_o must be 0, 1 or 2");
     g_fuse_attn_o = on;
     return ARC_OK;
 }

@@ -281,7 +281,9 @@ int arc_tune_decode(int kind, int bs, int rpl, int waves);
 int arc_tune_prefill_attention(int mfma);
 /* Tuning hook: 1 (default) runs each layer's attention and o projection of
  * decode steps captured later on this host thread as one launch, whose o
- * workgroups wait (bounded) for the attention's output; 0 as two launches. */
+ * workgroups wait (bounded) for the attention's output; 0 as two launches;
+ * 2 (test of the bounded wait) as one launch whose attention never signals:
+ * every wait gives up and the decode call returns ARC_ERR_DEVICE. */
 int arc_tune_fuse_attn_o(int on);
 
 /* Diagnostic: streaming read of `bytes` (16-byte aligned) with `grid`

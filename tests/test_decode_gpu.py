@@ -215,6 +215,35 @@ def test_attention_o_one_launch_matches_two_launches():
             assert np.array_equal(tf, tu)
 
 
+def test_attention_o_wait_gives_up_and_reports_an_error():
+    """The bounded wait of the attention + o launch: with the attention made
+    to withhold its signal (a host setting; every kernel still runs to its
+    end), each o workgroup's wait gives up after its poll limit and the
+    decode call returns an error naming the expired waits; the session then
+    decodes normally again, with the tokens of a fresh session."""
+    d = tiny_dims(layers=2)
+    T = arc.synth_model_tensors(d, SEED + 13)
+    model = arc.Model(d, T)
+    ref = arc.Session(model, 128)
+    ref.fill_kv(40, 3)
+    want, _ = ref.decode(7, 40, 4)
+    s = arc.Session(model, 128)
+    s.fill_kv(40, 3)
+    arc.tune_fuse_attn_o(2)
+    try:
+        with pytest.raises(arc.ArcError, match="gave up"):
+            s.decode(7, 40, 1)
+    finally:
+        arc.tune_fuse_attn_o(True)
+    s2 = arc.Session(model, 128)
+    s2.fill_kv(40, 3)
+    got, nf = s2.decode(7, 40, 4)
+    assert nf == 0 and np.array_equal(got, want)
+    s.fill_kv(40, 3)
+    again, nf = s.decode(7, 40, 4, graph=False)
+    assert nf == 0 and np.array_equal(again, want)
+
+
 def test_decode_rejects_bad_requests():
     d = tiny_dims(layers=1)
     model = arc.Model(d, seed=3)
