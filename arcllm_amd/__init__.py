@@ -94,6 +94,7 @@ _SIGS = {
     "arc_tune_prefill_attention": [C.c_int],
     "arc_probe_read": [_P, C.c_size_t, _P, _U32, _P],
     "arc_probe_read_unrolled": [_P, C.c_size_t, _P, _U32, C.c_int, _P],
+    "arc_probe_read_nt": [_P, C.c_size_t, _P, _U32, _P],
     "arc_exec148_materialize": [_P, _U32, _U32, _P, _P],
     "arc_exec148_validate": [_P, _P, _U32, _U32, C.POINTER(_U64), _P],
     "arc_exec148_validate_many": [C.POINTER(_P), C.POINTER(_P), _U32, _U32, _U32, C.POINTER(_U64), _P],
@@ -424,6 +425,11 @@ def probe_read_unrolled(buf, nbytes: int, out, grid: int = 2048, loads: int = 4,
                         stream: Optional[Stream] = None) -> None:
     """The streaming-read probe with `loads` independent 16-byte loads per lane in flight."""
     check(lib().arc_probe_read_unrolled(_ptr(buf), nbytes, _ptr(out), grid, loads, _sp(stream)))
+
+
+def probe_read_nt(buf, nbytes: int, out, grid: int = 2048, stream: Optional[Stream] = None) -> None:
+    """The one-load streaming-read probe with non-temporal loads."""
+    check(lib().arc_probe_read_nt(_ptr(buf), nbytes, _ptr(out), grid, _sp(stream)))
 
 
 def attention_workspace_bytes(kv_heads: int, hpk: int) -> int:

@@ -297,17 +297,21 @@ def load_traffic() -> dict:
 def ceiling(nbytes: int, banks: int, stream: arc.Stream, iters: int) -> tuple:
     """Streaming-read ceiling at `nbytes` per launch, rotating over `banks`
     initialised buffers: arc_probe_read_unrolled (coalesced 16 B loads, 1, 2,
-    4 or 8 independent loads per lane in flight) at 2048 / 4096 / 8192
-    workgroups.  Returns (best GB/s, {loads: best GB/s over the grids})."""
+    4 or 8 independent loads per lane in flight) and arc_probe_read_nt (one
+    load, non-temporal) at 2048 / 4096 / 8192 workgroups.  Returns (best
+    GB/s, {variant: best GB/s over the grids})."""
     n = nbytes // 4096 * 4096
     bufs = [arc.DeviceBuffer(n) for _ in range(banks)]
     for b in bufs:
         arc.check(arc.lib().arc_memset(b.ptr, 1, n, stream.handle))
     out = arc.DeviceBuffer(8192 * 256 * 4)
     per = {}
-    for loads in (1, 2, 4, 8):
+    for loads in (1, 2, 4, 8, "nt"):
         for grid in (2048, 4096, 8192):
-            fn = lambda i: arc.probe_read_unrolled(bufs[i % banks], n, out, grid, loads, stream)  # noqa: E731
+            if loads == "nt":
+                fn = lambda i: arc.probe_read_nt(bufs[i % banks], n, out, grid, stream)  # noqa: E731
+            else:
+                fn = lambda i: arc.probe_read_unrolled(bufs[i % banks], n, out, grid, loads, stream)  # noqa: E731
             time_loop(fn, 20, stream)
             ms = time_loop(fn, iters, stream)
             per[loads] = max(per.get(loads, 0.0), n / (ms / 1e3) / 1e9)
@@ -515,8 +519,8 @@ def main() -> int:
         "kernels": kernels,
         "stream_ceiling": {
             "kernel": "arc_probe_read_unrolled (coalesced 16 B/lane streaming read of initialised buffers, 1/2/4/8 "
-                      "independent loads per lane in flight, same bank rotation, best of 2048/4096/8192 "
-                      "workgroups)",
+                      "independent loads per lane in flight) and arc_probe_read_nt (one non-temporal load per "
+                      "lane in flight), same bank rotation, best of 2048/4096/8192 workgroups",
             "GB/s_at_step_bytes": round(ceil_step, 1),
             "GB/s_at_step_bytes_by_loads_in_flight": ceil_step_per,
             "GB/s_at_roofline_kernel_bytes": round(ceil_dom, 1),

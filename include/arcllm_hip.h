@@ -295,6 +295,10 @@ int arc_probe_read(const void *p, size_t bytes, uint32_t *out, uint32_t grid, ar
  * measurement aid of this build. */
 int arc_probe_read_unrolled(const void *p, size_t bytes, uint32_t *out, uint32_t grid, int loads,
                             arc_stream_t stream);
+/* The one-load probe with the non-temporal cache policy on its loads (the
+ * same chunks folded into the same outputs as arc_probe_read).  No
+ * counterpart in the reference: a measurement aid of this build. */
+int arc_probe_read_nt(const void *p, size_t bytes, uint32_t *out, uint32_t grid, arc_stream_t stream);
 
 /* ------------------------------------------------------ synthetic inputs */
 /* Host-side, deterministic generators for seeded synthetic packed tensors

@@ -497,3 +497,24 @@ def test_padded_q6_lmhead_bit_identical():
     t1, n1, l1 = _lmhead(arc.Q6_K, dev(w), rows, K, h, nw)
     t2, n2, l2 = _lmhead(arc.Q6_K_PADDED, dev(_pad_q6(w, rows, K)), rows, K, h, nw)
     assert (t1, n1) == (t2, n2) and same_bits(l1, l2)
+
+
+def test_stream_probes_fold_the_same_chunks():
+    """The streaming-read probes behind the bench's stream ceiling read what
+    they are given: the plain and the non-temporal probe fold the same 16-byte
+    chunks into the same per-thread words, equal to the fold computed here,
+    for a size that is not a multiple of the grid's stride."""
+    grid = 8
+    n16 = grid * 256 * 3 + 77
+    rng = np.random.default_rng(5)
+    host = rng.integers(0, 2**32, size=n16 * 4, dtype=np.uint64).astype(np.uint32)
+    buf = dev(host)
+    want = np.zeros(grid * 256, dtype=np.uint32)
+    chunks = np.bitwise_xor.reduce(host.reshape(n16, 4), axis=1)
+    for i in range(n16):
+        want[i % (grid * 256)] ^= chunks[i]
+    o1, o2 = arc.DeviceBuffer(grid * 256 * 4), arc.DeviceBuffer(grid * 256 * 4)
+    arc.probe_read(buf, n16 * 16, o1, grid)
+    arc.probe_read_nt(buf, n16 * 16, o2, grid)
+    assert np.array_equal(o1.download(np.uint32), want)
+    assert np.array_equal(o2.download(np.uint32), want)
